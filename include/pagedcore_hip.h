@@ -1,0 +1,115 @@
+/*
+ * pagedcore_hip.h — C ABI of the MI355X (gfx950) paged KV-cache hot path.
+ *
+ * The library moves and reads the KV pool that PagedCore's Python layer owns:
+ *
+ *   pool: fp16, contiguous [22 layers][2 kinds: K, V][num_blocks][16 slots][4 kv heads][64 dims]
+ *
+ * Element (layer, kind, block, slot, head, dim) lives at
+ *   ((((layer * 2 + kind) * num_blocks + block) * 16 + slot) * 256 + head * 64 + dim).
+ *
+ * Conventions shared by every entry point:
+ *   - return 0 on success, a nonzero pc_status otherwise; pc_last_error() then names the
+ *     problem (thread-local text, valid until the next call on the same thread);
+ *   - every pointer is device memory, except where stated; nothing here allocates or frees;
+ *   - work is only enqueued on `stream` (a hipStream_t passed as void*); no call synchronizes;
+ *   - all arguments are validated before anything is enqueued, so a failed call leaves the
+ *     pool untouched.
+ */
+#ifndef PAGEDCORE_HIP_H
+#define PAGEDCORE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum pc_status {
+  PC_OK = 0,
+  PC_ERR_ARGUMENT = 1, /* a size, index, pointer or alignment is invalid */
+  PC_ERR_LAUNCH = 2,   /* the HIP runtime rejected a kernel launch */
+};
+
+/* ABI revision; bumped whenever a signature or a layout contract changes. */
+int pc_abi_version(void);
+
+/* Text describing the last failure on the calling thread ("" if none). */
+const char* pc_last_error(void);
+
+/*
+ * KV append: copy K and V token rows into the pool through a slot mapping.
+ *
+ * Replaces the chunked `Tensor.copy_` loop of KVAllocator.append
+ * (reference src/pagedcore/kv_cache.py:161-172) and the per-row copies of
+ * KVAllocator.write_decode_layer (reference src/pagedcore/kv_cache.py:242-245).
+ *
+ * For src layer l in [0, num_layers) and token t in [0, num_tokens):
+ *   pool[layer_begin + l][0][slot / 16][slot % 16][:][:] = key  [l][t][:][:]
+ *   pool[layer_begin + l][1][slot / 16][slot % 16][:][:] = value[l][t][:][:]
+ * with slot = slot_mapping[t] = block * 16 + offset. A negative slot skips the token.
+ * The copy moves raw 16-bit words, so the pool bytes equal the source bytes.
+ *
+ * key/value rows are [4][64] fp16 with contiguous heads and dims; the layer and token
+ * strides (in fp16 elements) are free, so strided views need no staging copy.
+ * Every slot must be < num_blocks * 16 (checked on the device; out-of-range tokens are
+ * skipped, never written).
+ */
+int pc_kv_append(void* pool, int64_t num_blocks, int32_t layer_begin, int32_t num_layers,
+                 const void* key, int64_t key_layer_stride, int64_t key_token_stride,
+                 const void* value, int64_t value_layer_stride, int64_t value_token_stride,
+                 const int64_t* slot_mapping, int64_t num_tokens, void* stream);
+
+/*
+ * Paged decode attention for one layer, one query token per sequence.
+ *
+ * Replaces the two page traversals of paged_attention
+ * (reference src/pagedcore/attention.py:14-53) and the Python page generator that feeds
+ * them, KVAllocator.iter_layer_blocks (reference src/pagedcore/kv_cache.py:248-270): the
+ * block table is walked inside the kernel.
+ *
+ *   query        [batch][32][64] fp16, contiguous; q head h reads kv head h / 8
+ *   out          [batch][32][64] fp16, contiguous
+ *   block_tables [batch][max_blocks] int32 physical block ids (row b lists sequence b's
+ *                blocks in logical order; only the first ceil(len/16) are read)
+ *   context_lens [batch] int32, each in [1, max_blocks * 16]
+ *   out[b][h] = softmax(q[b][h] . K[b][:len]^T / 8) . V[b][:len], computed in fp32 and
+ *   rounded once to fp16. Slots past len are never multiplied, so poisoned (NaN) tail
+ *   slots do not reach the output.
+ *
+ * Long contexts are split into partitions of `partition_blocks` blocks (a multiple of 4,
+ * 4..128); partials go to the fp32 workspace and a second kernel merges them. Workspace:
+ *   ws_out [batch][32][max_partitions][64] fp32, ws_ml [batch][32][max_partitions][2] fp32,
+ *   max_partitions = ceil(max_blocks / partition_blocks)  (see pc_attn_workspace_floats).
+ * The workspace is scratch: no contents need to survive between calls.
+ */
+int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t num_blocks,
+                         int32_t layer, const int32_t* block_tables, int32_t max_blocks,
+                         const int32_t* context_lens, int32_t batch, int32_t partition_blocks,
+                         float* ws_out, float* ws_ml, void* stream);
+
+/* The two kernels of pc_paged_decode_attn, launched separately (same arguments). The
+ * partition kernel writes `out` directly for sequences that fit in one partition; the
+ * reduce kernel merges the others. Exposed so callers can time or order them apart. */
+int pc_paged_decode_attn_partitions(void* out, const void* query, const void* pool,
+                                    int64_t num_blocks, int32_t layer,
+                                    const int32_t* block_tables, int32_t max_blocks,
+                                    const int32_t* context_lens, int32_t batch,
+                                    int32_t partition_blocks, float* ws_out, float* ws_ml,
+                                    void* stream);
+int pc_paged_decode_attn_reduce(void* out, const int32_t* context_lens, int32_t batch,
+                                int32_t max_blocks, int32_t partition_blocks,
+                                const float* ws_out, const float* ws_ml, void* stream);
+
+/* Workspace size in floats for ws_out + ws_ml together (ws_ml starts after ws_out,
+ * at offset batch * 32 * max_partitions * 64); 0 on invalid arguments. */
+int64_t pc_attn_workspace_floats(int32_t batch, int32_t max_blocks, int32_t partition_blocks);
+
+/* Default partition size (blocks) used by the Python layer. */
+int32_t pc_attn_default_partition_blocks(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGEDCORE_HIP_H */

@@ -1,0 +1,529 @@
+"""KV pool, reservation-aware block allocator and the staged block gather.
+
+Drop-in for the reference's src/pagedcore/kv_cache.py: the pool layout, the allocator's
+public methods, its LIFO block choice, error types/messages and its publish-after-write /
+staged-decode semantics are the same. What changes is where the bytes move: every write
+into the pool is one launch of the HIP `pc_kv_append` kernel (all layers and tokens of a
+call at once) instead of a Python loop of `Tensor.copy_` calls, and attention reads the
+pool through device block tables built here (`gather_block_tables`) instead of a page
+generator.
+
+Additions to the reference API (additive, for batched callers):
+  * ``write_decode_layers`` writes one layer of a staged decode step for many requests in
+    one launch;
+  * ``gather_block_tables`` returns the device block table and context lengths that the
+    attention kernel walks, with the same staged-layer rules as ``iter_layer_blocks``;
+  * ``KVAllocator(pool, kv_writer=...)`` lets host-logic tests substitute the writer.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Iterator
+from contextlib import contextmanager
+from dataclasses import dataclass
+from itertools import chain
+from threading import current_thread
+from typing import Dict, Optional, Protocol, Sequence, Tuple
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from pagedcore_amd import _hip
+from pagedcore_amd.config import PagedCoreConfig
+from pagedcore_amd.engine_types import BlockId, BlockTable, CapacityCounts, KVReservation, RequestId
+
+LAYERS = 22
+BLOCK_TOKENS = 16
+KV_HEADS = 4
+HEAD_DIM = 64
+CONTEXT_LIMIT = 2048
+MAX_BLOCKS_PER_REQUEST = CONTEXT_LIMIT // BLOCK_TOKENS  # 128
+
+
+def allocate_kv_pool(config: PagedCoreConfig, *, device: str | torch.device = "cuda:0") -> Tensor:
+    """Allocate the fp16 pool [22, 2, blocks, 16, 4, 64] once; keep it for the worker's life.
+
+    Same sizing and memory checks as the reference (src/pagedcore/kv_cache.py:17-47):
+    whole 352 KiB blocks within ``kv_pool_mib``, free memory for pool + margin checked
+    before, margin re-checked after. Storage is uninitialised.
+    """
+    target = torch.device(device)
+    if target.type != "cuda":
+        raise ValueError("KV pool requires a CUDA device")
+    if not torch.cuda.is_available():
+        raise RuntimeError("KV pool requires an available CUDA runtime")
+
+    pool_bytes = config.kv_pool_mib * 2**20
+    margin_bytes = config.workspace_margin_mib * 2**20
+    block_bytes = LAYERS * 2 * config.block_tokens * KV_HEADS * HEAD_DIM * 2
+    num_blocks = pool_bytes // block_bytes
+    free_bytes, _ = torch.cuda.mem_get_info(target)
+    if free_bytes < pool_bytes + margin_bytes:
+        raise RuntimeError("configured KV pool and workspace margin do not fit in GPU memory")
+
+    pool = torch.empty(
+        (LAYERS, 2, num_blocks, config.block_tokens, KV_HEADS, HEAD_DIM),
+        dtype=torch.float16,
+        device=target,
+    )
+    if torch.cuda.mem_get_info(target)[0] < margin_bytes:
+        del pool
+        raise RuntimeError("KV pool allocation leaves less than the configured workspace margin")
+    return pool
+
+
+class KVWriter(Protocol):
+    """Moves token rows into the pool: pool[layer_begin + l, 0/1, s // 16, s % 16] = K/V[l, t]."""
+
+    def append(
+        self, pool: Tensor, layer_begin: int, key: Tensor, value: Tensor, slots: Sequence[int]
+    ) -> None: ...
+
+
+class HipKVWriter:
+    """The GPU data path: one `pc_kv_append` launch per call, on the current stream."""
+
+    def __init__(self) -> None:
+        _hip.load()  # fail at construction, not at the first write
+
+    def append(
+        self, pool: Tensor, layer_begin: int, key: Tensor, value: Tensor, slots: Sequence[int]
+    ) -> None:
+        if isinstance(slots, Tensor):
+            slot_mapping = slots
+        else:
+            slot_mapping = torch.as_tensor(np.asarray(slots, dtype=np.int64)).to(pool.device)
+        _hip.kv_append(pool, layer_begin, key, value, slot_mapping)
+
+
+class _HostOnlyWriter:
+    """Stand-in for CPU pools: bookkeeping works, moving KV bytes does not."""
+
+    def append(self, pool: Tensor, layer_begin: int, key: Tensor, value: Tensor, slots: Sequence[int]) -> None:
+        raise RuntimeError(
+            "KV writes run on the GPU: this allocator's pool is on the CPU and has no KV writer"
+        )
+
+
+@dataclass(frozen=True, slots=True)
+class _SequenceCache:
+    reservation: KVReservation
+    blocks: BlockTable = ()
+    length: int = 0
+
+
+@dataclass(slots=True)
+class _TokenAppend:
+    sequence: _SequenceCache
+    written_layers: int = 0
+
+
+def _slot_mapping(blocks: BlockTable, start: int, count: int) -> np.ndarray:
+    """Pool slot (block * 16 + offset) of positions start .. start + count - 1."""
+    positions = np.arange(start, start + count, dtype=np.int64)
+    table = np.asarray(blocks, dtype=np.int64)
+    return table[positions // BLOCK_TOKENS] * BLOCK_TOKENS + positions % BLOCK_TOKENS
+
+
+class KVAllocator:
+    """Assign blocks within an existing pool; construct and use on the model worker.
+
+    CUDA work stays on the stream current at construction. Block reads borrow pool
+    storage: treat them as read-only and do not keep them past an append or release.
+    CPU pools support the bookkeeping (tests); their KV writes need an explicit writer.
+    """
+
+    def __init__(self, pool: Tensor, *, kv_writer: Optional[KVWriter] = None) -> None:
+        if (
+            pool.ndim != 6
+            or pool.shape[:2] != (LAYERS, 2)
+            or pool.shape[2] < 1
+            or pool.shape[3:] != (BLOCK_TOKENS, KV_HEADS, HEAD_DIM)
+            or pool.dtype != torch.float16
+            or pool.device.type not in ("cpu", "cuda")
+            or not pool.is_contiguous()
+            or pool.requires_grad
+        ):
+            raise ValueError("KV pool must be contiguous FP16 [22, 2, blocks, 16, 4, 64] storage")
+        if kv_writer is None:
+            kv_writer = HipKVWriter() if pool.is_cuda else _HostOnlyWriter()
+        self._pool = pool
+        self._writer = kv_writer
+        self._worker = current_thread()
+        self._stream = torch.cuda.current_stream(pool.device) if pool.is_cuda else None
+        self._free_blocks = [BlockId(index) for index in reversed(range(pool.shape[2]))]
+        self._sequences: Dict[RequestId, _SequenceCache] = {}
+        # Tables are checked against the owners recorded when blocks are assigned.
+        self._block_owners: Dict[BlockId, RequestId] = {}
+        self._decode_appends: Optional[Dict[RequestId, _TokenAppend]] = None
+        # Bumped whenever a table or length may change; keys the device-table cache.
+        self._version = 0
+        self._table_cache: Dict[tuple, Tuple[Tensor, Tensor]] = {}
+        self._decode_slot_cache: Dict[Tuple[RequestId, ...], Tensor] = {}
+
+    @property
+    def pool(self) -> Tensor:
+        return self._pool
+
+    def create(self, reservation: KVReservation) -> None:
+        """Grant credits at admission without assigning physical blocks."""
+        self._check_mutation()
+        request_id = reservation.request_id
+        if request_id in self._sequences:
+            raise ValueError("request already has a KV cache")
+        counts = self.capacity()
+        if reservation.maximum_block_credits > counts.total_blocks:
+            raise ValueError("reservation exceeds total KV pool capacity")
+        if reservation.maximum_block_credits > MAX_BLOCKS_PER_REQUEST:
+            raise ValueError("reservation exceeds KV context capacity")
+        if reservation.maximum_block_credits > counts.total_blocks - counts.reserved_blocks:
+            raise RuntimeError("KV pool has insufficient unreserved blocks")
+        self._sequences[request_id] = _SequenceCache(reservation)
+        self._touch()
+        self._assert_accounting()
+
+    def capacity(self) -> CapacityCounts:
+        """Snapshot ownership and credits, including requests awaiting cleanup."""
+        self._check_worker()
+        return self._assert_accounting()
+
+    def block_table(self, request_id: RequestId) -> BlockTable:
+        self._check_worker()
+        self._assert_accounting()
+        return self._sequences[request_id].blocks
+
+    def cached_length(self, request_id: RequestId) -> int:
+        self._check_worker()
+        self._assert_accounting()
+        return self._sequences[request_id].length
+
+    @torch.inference_mode()
+    def append(self, request_id: RequestId, key: Tensor, value: Tensor) -> None:
+        """Append rotated K and unrotated V, each FP16 [22, tokens, 4, 64].
+
+        All checks run before the launch; the new length and blocks are published only
+        after the launch was accepted, so a failed write leaves ownership and the valid
+        positions unchanged (unpublished slots may be dirty).
+        """
+        self._check_mutation()
+        self._assert_accounting()
+        sequence = self._sequences[request_id]
+        if (
+            key.ndim != 4
+            or key.shape[0] != LAYERS
+            or key.shape[1] < 1
+            or key.shape[2:] != (KV_HEADS, HEAD_DIM)
+            or value.shape != key.shape
+            or key.dtype != torch.float16
+            or value.dtype != torch.float16
+            or key.device != self._pool.device
+            or value.device != self._pool.device
+        ):
+            raise ValueError("K and V must share FP16 [22, tokens, 4, 64] on the pool device")
+        length = sequence.length + key.shape[1]
+        if length > CONTEXT_LIMIT:
+            raise ValueError("KV cache must not exceed 2048 token positions")
+        required = (length + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+        if required > sequence.reservation.maximum_block_credits:
+            raise RuntimeError("KV append exceeds request reservation")
+        additional = required - len(sequence.blocks)
+        if additional > len(self._free_blocks):
+            raise RuntimeError("KV pool has insufficient free blocks")
+        new_blocks = tuple(reversed(self._free_blocks[-additional:])) if additional else ()
+        blocks = sequence.blocks + new_blocks
+
+        self._writer.append(self._pool, 0, key, value, _slot_mapping(blocks, sequence.length, key.shape[1]))
+
+        # Publish valid positions only after the K and V writes have been issued.
+        if additional:
+            del self._free_blocks[-additional:]
+        self._block_owners.update((block, request_id) for block in new_blocks)
+        self._sequences[request_id] = _SequenceCache(sequence.reservation, blocks, length)
+        self._touch()
+        self._assert_accounting()
+
+    @contextmanager
+    def append_decode(self, request_ids: Tuple[RequestId, ...]) -> Iterator[None]:
+        """Stage one token per request; commit only if all 22 layers were written.
+
+        Blocks for requests at a 16-token boundary are borrowed from the free-list tail in
+        request order and only removed from it on commit; any exception discards the
+        staged state (reference src/pagedcore/kv_cache.py:181-219).
+        """
+        self._check_mutation()
+        self._assert_accounting()
+        if not request_ids or len(set(request_ids)) != len(request_ids):
+            raise ValueError("decode requires nonempty, distinct request IDs")
+        appends: Dict[RequestId, _TokenAppend] = {}
+        additional = 0
+        for request_id in request_ids:
+            sequence = self._sequences[request_id]
+            if not 1 <= sequence.length < CONTEXT_LIMIT:
+                raise ValueError("decode requires 1 to 2047 cached token positions")
+            length = sequence.length + 1
+            blocks = sequence.blocks
+            if (length + BLOCK_TOKENS - 1) // BLOCK_TOKENS > sequence.reservation.maximum_block_credits:
+                raise RuntimeError("KV append exceeds request reservation")
+            if sequence.length % BLOCK_TOKENS == 0:
+                additional += 1
+                if additional > len(self._free_blocks):
+                    raise RuntimeError("KV pool has insufficient free blocks")
+                blocks += (self._free_blocks[-additional],)
+            appends[request_id] = _TokenAppend(_SequenceCache(sequence.reservation, blocks, length))
+
+        # Block other mutations while free-list entries are borrowed for staged writes.
+        self._decode_appends = appends
+        self._touch()
+        try:
+            yield
+            if any(append.written_layers != LAYERS for append in appends.values()):
+                raise RuntimeError("decode must write every cache layer before committing")
+            if additional:
+                del self._free_blocks[-additional:]
+            for request_id, append in appends.items():
+                original = self._sequences[request_id]
+                for block in append.sequence.blocks[len(original.blocks) :]:
+                    self._block_owners[block] = request_id
+                self._sequences[request_id] = append.sequence
+            self._assert_accounting()
+        finally:
+            self._decode_appends = None
+            self._touch()
+
+    @torch.inference_mode()
+    def write_decode_layer(
+        self, request_id: RequestId, layer_index: int, key: Tensor, value: Tensor
+    ) -> None:
+        """Write one token's rotated K / unrotated V, FP16 [4, 64], in layer order."""
+        self._check_worker()
+        self._assert_accounting()
+        if self._decode_appends is None:
+            raise RuntimeError("decode writes require a staged append")
+        append = self._decode_appends[request_id]
+        if type(layer_index) is not int or not 0 <= layer_index < LAYERS:
+            raise ValueError("layer_index must identify one of the 22 decoder layers")
+        if layer_index != append.written_layers:
+            raise ValueError("decode cache layers must be written once in order")
+        if any(
+            tensor.shape != (KV_HEADS, HEAD_DIM)
+            or tensor.dtype != torch.float16
+            or tensor.device != self._pool.device
+            for tensor in (key, value)
+        ):
+            raise ValueError("K and V must share FP16 [4, 64] on the pool device")
+        logical_block, slot = divmod(append.sequence.length - 1, BLOCK_TOKENS)
+        block = append.sequence.blocks[logical_block]
+        self._writer.append(self._pool, layer_index, key[None, None], value[None, None], [block * BLOCK_TOKENS + slot])
+        append.written_layers += 1
+
+    @torch.inference_mode()
+    def write_decode_layers(
+        self,
+        request_ids: Tuple[RequestId, ...],
+        layer_index: int,
+        key: Tensor,
+        value: Tensor,
+    ) -> None:
+        """Batched write_decode_layer: row b of FP16 [B, 4, 64] K/V goes to request_ids[b].
+
+        Every row is checked before the single launch; written layers advance together.
+        """
+        self._check_worker()
+        self._assert_accounting()
+        if self._decode_appends is None:
+            raise RuntimeError("decode writes require a staged append")
+        if not request_ids or len(set(request_ids)) != len(request_ids):
+            raise ValueError("decode requires nonempty, distinct request IDs")
+        appends = [self._decode_appends[request_id] for request_id in request_ids]
+        if type(layer_index) is not int or not 0 <= layer_index < LAYERS:
+            raise ValueError("layer_index must identify one of the 22 decoder layers")
+        if any(layer_index != append.written_layers for append in appends):
+            raise ValueError("decode cache layers must be written once in order")
+        if any(
+            tensor.shape != (len(request_ids), KV_HEADS, HEAD_DIM)
+            or tensor.dtype != torch.float16
+            or tensor.device != self._pool.device
+            for tensor in (key, value)
+        ):
+            raise ValueError("K and V must share FP16 [batch, 4, 64] on the pool device")
+        slots = self._decode_slots(request_ids, appends)
+        self._writer.append(self._pool, layer_index, key[None], value[None], slots)
+        for append in appends:
+            append.written_layers += 1
+
+    def _decode_slots(self, request_ids: Tuple[RequestId, ...], appends: Sequence[_TokenAppend]):
+        """Slot of each staged token; a device tensor cached for the decode step on GPU pools."""
+        cached = self._decode_slot_cache.get(request_ids)
+        if cached is not None:
+            return cached
+        slots = np.empty(len(appends), dtype=np.int64)
+        for row, append in enumerate(appends):
+            logical_block, slot = divmod(append.sequence.length - 1, BLOCK_TOKENS)
+            slots[row] = append.sequence.blocks[logical_block] * BLOCK_TOKENS + slot
+        if not self._pool.is_cuda:
+            return slots
+        device_slots = torch.from_numpy(slots).to(self._pool.device)
+        self._decode_slot_cache[request_ids] = device_slots
+        return device_slots
+
+    def iter_layer_blocks(
+        self, request_id: RequestId, *, layer_index: int
+    ) -> Iterator[Tuple[Tensor, Tensor]]:
+        """Borrow valid [slots, 4, 64] pages, including a completed staged layer."""
+        sequence = self._layer_sequence(request_id, layer_index)
+        for logical_block, physical_block in enumerate(sequence.blocks):
+            self._check_worker()
+            valid = min(BLOCK_TOKENS, sequence.length - logical_block * BLOCK_TOKENS)
+            yield (
+                self._pool[layer_index, 0, physical_block, :valid],
+                self._pool[layer_index, 1, physical_block, :valid],
+            )
+
+    def _layer_sequence(self, request_id: RequestId, layer_index: int) -> _SequenceCache:
+        """The table/length attention must read for a layer (the staged gather rules).
+
+        Same checks and order as the reference's iter_layer_blocks
+        (src/pagedcore/kv_cache.py:252-263): worker, accounting, layer index, unknown
+        request (KeyError), unwritten staged layer (RuntimeError), empty cache (ValueError).
+        """
+        self._check_worker()
+        self._assert_accounting()
+        if type(layer_index) is not int or not 0 <= layer_index < LAYERS:
+            raise ValueError("layer_index must identify one of the 22 decoder layers")
+        return self._staged_sequence(request_id, layer_index)
+
+    def _staged_sequence(self, request_id: RequestId, layer_index: int) -> _SequenceCache:
+        sequence = self._sequences[request_id]
+        if self._decode_appends is not None and request_id in self._decode_appends:
+            append = self._decode_appends[request_id]
+            if layer_index >= append.written_layers:
+                raise RuntimeError("cannot read an unwritten decode layer")
+            sequence = append.sequence
+        if sequence.length == 0:
+            raise ValueError("attention requires a nonempty cache")
+        return sequence
+
+    def gather_block_tables(
+        self, request_ids: Sequence[RequestId], *, layer_index: int
+    ) -> Tuple[Tensor, Tensor]:
+        """Device block tables int32 [B, W] and context lengths int32 [B] for a layer.
+
+        Row b lists request_ids[b]'s physical blocks in logical order (staged tables for
+        requests whose staged layer is written); W is the longest table in the batch.
+        Cached per allocator state, so the 22 layers of a decode step share one upload.
+        """
+        if not request_ids:
+            raise ValueError("attention requires at least one request")
+        self._check_worker()
+        self._assert_accounting()
+        if type(layer_index) is not int or not 0 <= layer_index < LAYERS:
+            raise ValueError("layer_index must identify one of the 22 decoder layers")
+        sequences = [self._staged_sequence(request_id, layer_index) for request_id in request_ids]
+        staged = self._decode_appends is not None
+        key = (self._version, tuple(request_ids), staged)
+        cached = self._table_cache.get(key)
+        if cached is not None:
+            return cached
+        width = max(len(sequence.blocks) for sequence in sequences)
+        tables = np.zeros((len(sequences), width), dtype=np.int32)
+        lengths = np.empty(len(sequences), dtype=np.int32)
+        for row, sequence in enumerate(sequences):
+            tables[row, : len(sequence.blocks)] = sequence.blocks
+            lengths[row] = sequence.length
+        result = (
+            torch.from_numpy(tables).to(self._pool.device),
+            torch.from_numpy(lengths).to(self._pool.device),
+        )
+        if len(self._table_cache) > 64:
+            self._table_cache.clear()
+        self._table_cache[key] = result
+        return result
+
+    def read_block(self, request_id: RequestId, logical_block: int) -> Tuple[Tensor, Tensor]:
+        """Borrow K/V views [22, valid slots, 4, 64] for one logical block."""
+        self._check_worker()
+        self._assert_accounting()
+        sequence = self._sequences[request_id]
+        if type(logical_block) is not int or not 0 <= logical_block < len(sequence.blocks):
+            raise ValueError("logical block must identify a cached block")
+        physical_block = sequence.blocks[logical_block]
+        valid = min(BLOCK_TOKENS, sequence.length - logical_block * BLOCK_TOKENS)
+        return (
+            self._pool[:, 0, physical_block, :valid],
+            self._pool[:, 1, physical_block, :valid],
+        )
+
+    def release_all(self, request_id: RequestId) -> None:
+        """Release once on the worker stream; unknown/released requests raise KeyError."""
+        self._check_mutation()
+        self._assert_accounting()
+        sequence = self._sequences.pop(request_id)
+        for block in sequence.blocks:
+            del self._block_owners[block]
+        self._free_blocks.extend(reversed(sequence.blocks))
+        self._touch()
+        self._assert_accounting()
+
+    def _touch(self) -> None:
+        self._version += 1
+        self._table_cache.clear()
+        self._decode_slot_cache.clear()
+
+    def _check_mutation(self) -> None:
+        self._check_worker()
+        if self._decode_appends is not None:
+            raise RuntimeError("KV mutation is not allowed during a staged decode append")
+
+    def _check_worker(self) -> None:
+        if current_thread() is not self._worker:
+            raise RuntimeError("KV allocator must be used by its owning model worker")
+        if self._stream is not None and torch.cuda.current_stream(self._pool.device) != self._stream:
+            raise RuntimeError("KV allocator must use its owning CUDA stream")
+
+    def _assert_accounting(self) -> CapacityCounts:
+        """Full ownership invariants (reference src/pagedcore/kv_cache.py:314-357).
+
+        Same checks and messages; the per-block type/range scans run as C-level set and
+        min/max passes rather than a Python loop.
+        """
+        total = self._pool.shape[2]
+        for request_id, sequence in self._sequences.items():
+            if (
+                sequence.reservation.request_id != request_id
+                or type(sequence.length) is not int
+                or not 0 <= sequence.length <= CONTEXT_LIMIT
+                or type(sequence.blocks) is not tuple
+                or len(sequence.blocks) != (sequence.length + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+                or not len(sequence.blocks) <= sequence.reservation.maximum_block_credits <= MAX_BLOCKS_PER_REQUEST
+            ):
+                raise RuntimeError("corrupt KV block table or reservation")
+        assigned = [block for sequence in self._sequences.values() for block in sequence.blocks]
+        free_list = self._free_blocks
+        if free_list or assigned:
+            types = set(map(type, chain(free_list, assigned)))
+            if types != {int} or min(chain(free_list, assigned)) < 0 or max(chain(free_list, assigned)) >= total:
+                raise RuntimeError("invalid physical KV block")
+        owned = set(assigned)
+        free = set(free_list)
+        if len(assigned) != len(owned):
+            raise RuntimeError("physical KV blocks must have unique owners")
+        if len(free_list) != len(free):
+            raise RuntimeError("free KV blocks must be unique")
+        if not free.isdisjoint(owned):
+            raise RuntimeError("owned KV blocks must not be free")
+        if len(free) + len(owned) != total:
+            raise RuntimeError("KV blocks must cover the pool")
+        owners = {
+            block: request_id for request_id, sequence in self._sequences.items() for block in sequence.blocks
+        }
+        if owners != self._block_owners:
+            raise RuntimeError("KV blocks are not owned by the recorded requests")
+        return CapacityCounts(
+            total_blocks=total,
+            free_blocks=len(free_list),
+            owned_blocks=len(assigned),
+            reserved_blocks=sum(sequence.reservation.maximum_block_credits for sequence in self._sequences.values()),
+            active_slots=len(self._sequences),
+            live_cached_token_slots=sum(sequence.length for sequence in self._sequences.values()),
+        )

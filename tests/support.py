@@ -1,0 +1,54 @@
+"""Shared test helpers (not product code)."""
+
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from pagedcore_amd.engine_types import KVReservation, RequestId
+from pagedcore_amd.kv_cache import KVAllocator
+
+
+class CpuCopyWriter:
+    """Test double for the allocator's KV writer on CPU pools.
+
+    Performs the same pool writes as the HIP kernel with tensor indexing, and can fail on
+    its N-th call to exercise the allocator's rollback (the GPU path's single launch per
+    call makes "fail at call N" the natural injection point).
+    """
+
+    def __init__(self, fail_at: Optional[int] = None) -> None:
+        self.calls = 0
+        self.fail_at = fail_at
+
+    def append(self, pool: Tensor, layer_begin: int, key: Tensor, value: Tensor, slots: Sequence[int]) -> None:
+        self.calls += 1
+        if self.fail_at is not None and self.calls == self.fail_at:
+            raise RuntimeError("injected copy failure")
+        slots = torch.as_tensor(np.asarray(slots, dtype=np.int64))
+        blocks, offsets = slots // 16, slots % 16
+        layers = slice(layer_begin, layer_begin + key.shape[0])
+        pool[layers, 0, blocks, offsets] = key
+        pool[layers, 1, blocks, offsets] = value
+
+
+def cpu_allocator(pool: Tensor, writer: Optional[CpuCopyWriter] = None) -> KVAllocator:
+    return KVAllocator(pool, kv_writer=writer if writer is not None else CpuCopyWriter())
+
+
+def kv_values(tokens: int, start: int = 0, device: str | torch.device = "cpu") -> tuple[Tensor, Tensor]:
+    """Distinct, exactly representable K/V [22, tokens, 4, 64] (V = -K - 1)."""
+    key = torch.arange(22 * tokens * 4 * 64, dtype=torch.float32).reshape(22, tokens, 4, 64)
+    key = (key / 256 + start).half().to(device)
+    return key, -key - 1
+
+
+def cached(allocator: KVAllocator, key: Tensor, value: Tensor, name: str = "attention") -> RequestId:
+    """Create a request holding exactly key/value's tokens."""
+    request = RequestId(name)
+    allocator.create(KVReservation(request, (key.shape[1] + 15) // 16))
+    allocator.append(request, key, value)
+    return request

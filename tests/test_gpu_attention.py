@@ -1,0 +1,357 @@
+"""Paged decode attention on the GPU vs the CPU oracle and the FP64 dense oracle.
+
+The reference's attention tests (tests/unit/test_attention.py, tests/gpu/test_attention_cuda.py)
+re-run against the HIP path through the unchanged Python API, plus the batched shapes the
+hot path is measured on. Tolerance: max-abs/rel 2e-3 on fp16 outputs (the reference's
+policy), tighter where the reference uses a tighter bound.
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_reference as ref
+from pagedcore_amd import _hip, workloads
+from pagedcore_amd.attention import paged_attention, paged_attention_batch
+from pagedcore_amd.engine_types import CapacityCounts, KVReservation, RequestId
+from pagedcore_amd.kv_cache import KVAllocator
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(atol=2e-3, rtol=2e-3)
+
+
+def _say(*parts) -> None:
+    print(*parts, flush=True)
+    sys.stdout.flush()
+
+
+def test_device_is_gfx950_and_one_hip_runtime_is_mapped(device):
+    name = torch.cuda.get_device_properties(device).gcnArchName
+    _say("device", torch.cuda.get_device_name(device), name)
+    assert name.startswith("gfx950")
+    _hip.load()
+    with open("/proc/self/maps") as maps:
+        runtimes = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    assert len(runtimes) == 1, runtimes
+    with open("/proc/self/maps") as maps:
+        assert any(_hip.LIBRARY_NAME in line for line in maps)
+
+
+def _fp64_half(query, key, value):
+    return ref.dense_attention_fp64(query, key, value).reshape(1, 32, 1, 64).half()
+
+
+def _check(query, key, value, *, layer, atol=2e-3, exact=None):
+    """The reference GPU harness (tests/gpu/test_attention_cuda.py:93-145) on the HIP path:
+    a NaN-poisoned pool with a retained sentinel request between released ones, so the
+    request's table is fragmented; checks FP64 and oracle agreement, autocast invariance,
+    untouched pool, unchanged table/length/accounting."""
+    device = query.device
+    tokens = key.shape[1]
+    blocks = (tokens + 15) // 16
+    pool = torch.full((22, 2, blocks + 3, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    for name in ("first", "retained", "last"):
+        request = RequestId(name)
+        allocator.create(KVReservation(request, 1))
+        sentinel = torch.full((22, 16, 4, 64), -100.0, dtype=torch.float16, device=device)
+        allocator.append(request, sentinel, -sentinel)
+    allocator.release_all(RequestId("first"))
+    allocator.release_all(RequestId("last"))
+    request = RequestId("attention")
+    allocator.create(KVReservation(request, blocks))
+    allocator.append(request, key, value)
+    table = allocator.block_table(request)
+    if blocks > 1:
+        assert table != tuple(range(table[0], table[0] + blocks))
+    before = pool.clone()
+    counts = allocator.capacity()
+
+    actual = paged_attention(query, allocator, request, layer_index=layer)
+    with torch.autocast("cuda", dtype=torch.float16):
+        autocast_actual = paged_attention(query, allocator, request, layer_index=layer)
+    torch.cuda.synchronize(device)
+
+    assert actual.device == query.device and actual.dtype == torch.float16
+    assert actual.shape == (1, 32, 1, 64) and not actual.requires_grad
+    assert torch.isfinite(actual).all()
+    expected = _fp64_half(query, key[layer], value[layer])
+    torch.testing.assert_close(actual.cpu(), expected, atol=atol, rtol=2e-3)
+    oracle = ref.reference_paged_attention(query.detach().cpu(), pool.cpu(), layer, list(table), tokens)
+    torch.testing.assert_close(actual.cpu(), oracle, atol=atol, rtol=2e-3)
+    if exact is not None:
+        assert torch.equal(actual.cpu(), torch.full_like(actual.cpu(), exact) if not callable(exact) else exact())
+    assert torch.equal(autocast_actual, actual)
+    torch.testing.assert_close(pool, before, atol=0, rtol=0, equal_nan=True)
+    assert allocator.block_table(request) == table
+    assert allocator.cached_length(request) == tokens
+    assert allocator.capacity() == counts
+    allocator.release_all(request)
+    allocator.release_all(RequestId("retained"))
+    assert allocator.capacity() == CapacityCounts(blocks + 3, blocks + 3, 0, 0, 0, 0)
+    return actual
+
+
+@pytest.mark.parametrize("tokens,layer", [(1, 0), (15, 21), (16, 7), (17, 0), (49, 21), (2048, 11)])
+def test_cache_boundaries_match_fp64_and_oracle(device, tokens, layer):
+    _say("boundaries", tokens, layer)
+    gen = torch.Generator(device=device).manual_seed(tokens)
+    key = torch.randn(22, tokens, 4, 64, dtype=torch.float16, device=device, generator=gen)
+    value = torch.randn(22, tokens, 4, 64, dtype=torch.float16, device=device, generator=gen)
+    query = torch.randn(1, 32, 1, 128, dtype=torch.float16, device=device, generator=gen)
+    _check(query[..., ::2].requires_grad_(), key, value, layer=layer)
+
+
+def test_eight_query_heads_map_to_each_kv_head(device):
+    key = torch.zeros(22, 33, 4, 64, dtype=torch.float16, device=device)
+    values = 100 * torch.arange(4, device=device)[None, :] + torch.arange(33, device=device)[:, None]
+    value = values[None, :, :, None].expand(22, 33, 4, 64).half()
+    out = _check(torch.zeros(1, 32, 1, 64, dtype=torch.float16, device=device), key, value, layer=21)
+    for head in range(32):
+        assert torch.equal(out[0, head, 0].cpu(), torch.full((64,), 100 * (head // 8) + 16).half())
+
+
+def test_tiny_probabilities_survive_until_value_accumulation(device):
+    key = torch.zeros(22, 17, 4, 64, dtype=torch.float16, device=device)
+    key[:, :, :, 0], key[:, 0, :, 0] = -160, 0
+    value = torch.full_like(key, 65504)
+    value[:, 0] = 0
+    query = torch.zeros(1, 32, 1, 64, dtype=torch.float16, device=device)
+    query[..., 0] = 1
+    out = _check(query, key, value, layer=0, atol=1e-6)
+    assert (out > 0).all()
+
+
+def test_rounds_only_after_value_cancellation_across_pages(device):
+    key = torch.zeros(22, 32, 4, 64, dtype=torch.float16, device=device)
+    value = torch.zeros_like(key)
+    value[:, 0], value[:, 1], value[:, 16] = 32768, 8, -32768
+    _check(torch.zeros(1, 32, 1, 64, dtype=torch.float16, device=device), key, value, layer=0, exact=0.25)
+
+
+def test_normalizes_all_scores_before_value_products(device):
+    # tests/unit/test_attention.py:182-221 (tables (0, 2) on a 3-block pool): exactly 3.
+    pool = torch.full((22, 2, 3, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    key = torch.zeros(22, 17, 4, 64, dtype=torch.float16, device=device)
+    value = torch.zeros_like(key)
+    value[:, :16], value[:, 16:] = 2, 19
+    request, blocker = RequestId("normalized"), RequestId("blocker")
+    allocator.create(KVReservation(request, 2))
+    allocator.append(request, key[:, :16], value[:, :16])
+    allocator.create(KVReservation(blocker, 1))
+    allocator.append(blocker, key[:, :16], torch.full_like(key[:, :16], 1000))
+    allocator.append(request, key[:, 16:], value[:, 16:])
+    assert allocator.block_table(request) == (0, 2)
+    before, counts = pool.clone(), allocator.capacity()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        actual = paged_attention(torch.zeros(1, 32, 1, 64, dtype=torch.float16, device=device), allocator, request, layer_index=0)
+    assert torch.equal(actual.cpu(), torch.full((1, 32, 1, 64), 3, dtype=torch.float16))
+    torch.testing.assert_close(pool, before, atol=0, rtol=0, equal_nan=True)
+    assert allocator.capacity() == counts
+
+
+@pytest.mark.parametrize("reverse", [False, True])
+@pytest.mark.parametrize("query_scale", [1.0, 1000.0])
+def test_large_block_scores_rescale_softmax(device, reverse, query_scale):
+    key = torch.full((22, 49, 4, 64), -1000.0, dtype=torch.float16, device=device)
+    key[:, 16:32] = 0
+    key[:, 32:] = 1000
+    value = torch.randn(key.shape, dtype=torch.float16, device=device, generator=torch.Generator(device=device).manual_seed(9))
+    if reverse:
+        key, value = key.flip(1), value.flip(1)
+    query = torch.full((1, 32, 1, 64), query_scale, dtype=torch.float16, device=device)
+    _check(query, key, value, layer=0)
+
+
+@pytest.mark.parametrize("state", ["unknown", "empty", "released"])
+def test_rejects_requests_without_cached_tokens(device, state):
+    allocator = KVAllocator(torch.empty(22, 2, 1, 16, 4, 64, dtype=torch.float16, device=device))
+    request = RequestId("missing")
+    if state != "unknown":
+        allocator.create(KVReservation(request, 1))
+    if state == "released":
+        allocator.release_all(request)
+    before = allocator.capacity()
+    with pytest.raises(ValueError if state == "empty" else KeyError):
+        paged_attention(torch.zeros(1, 32, 1, 64, dtype=torch.float16, device=device), allocator, request, layer_index=0)
+    assert allocator.capacity() == before
+
+
+def _upload_single_decode(device):
+    w = workloads.single_decode()
+    pool = torch.full((22, 2, w.num_blocks, 16, 4, 64), float("nan"), dtype=torch.float16)
+    for logical, physical in enumerate(w.table):
+        pool[w.layer, 0, physical] = torch.from_numpy(w.key[logical * 16 : logical * 16 + 16])
+        pool[w.layer, 1, physical] = torch.from_numpy(w.value[logical * 16 : logical * 16 + 16])
+    return w, pool.to(device)
+
+
+def test_config1_golden_through_the_c_abi(device):
+    """Single-sequence 128-token decode over a seeded random table of a 64-block pool, via
+    the raw C ABI; the committed FP64 output is the reference answer."""
+    golden = np.load(os.path.join(os.path.dirname(__file__), "golden", "config1_single_decode.npz"))
+    w, pool = _upload_single_decode(device)
+    assert np.array_equal(golden["query"], w.query.view(np.uint16))
+    assert np.array_equal(golden["key"], w.key.view(np.uint16))
+    assert golden["table"].tolist() == w.table
+    query = torch.from_numpy(w.query).to(device).reshape(1, 32, 64)
+    out = torch.empty(1, 32, 64, dtype=torch.float16, device=device)
+    tables = torch.tensor([w.table], dtype=torch.int32, device=device)
+    lens = torch.tensor([128], dtype=torch.int32, device=device)
+    for parts in (4, 8, 32):
+        out.fill_(float("nan"))
+        _hip.paged_decode_attention(out, query, pool, w.layer, tables, lens, partition_blocks=parts)
+        torch.cuda.synchronize()
+        expected = torch.from_numpy(golden["expected_fp64"]).reshape(1, 32, 64)
+        torch.testing.assert_close(out.cpu().double(), expected, atol=2e-3, rtol=2e-3)
+        torch.testing.assert_close(out.cpu(), expected.half(), **TOL)
+
+
+def _random_pool(device, num_blocks, seed):
+    gen = torch.Generator(device=device).manual_seed(seed)
+    return torch.randn((22, 2, num_blocks, 16, 4, 64), dtype=torch.float16, device=device, generator=gen)
+
+
+def _oracle_rows(pool, layer, w, queries, rows):
+    """Oracle outputs for selected rows, reading only those rows' blocks from the GPU."""
+    out = {}
+    for b in rows:
+        length = int(w.lengths[b])
+        table = w.tables[b, : (length + 15) // 16].tolist()
+        blocks = torch.tensor(table, dtype=torch.long, device=pool.device)
+        sub = torch.zeros((22, 2, len(table), 16, 4, 64), dtype=torch.float16)
+        sub[layer] = pool[layer].index_select(1, blocks).cpu()
+        q = queries[b : b + 1].reshape(1, 32, 1, 64).cpu()
+        out[b] = (
+            ref.reference_paged_attention(q, sub, layer, list(range(len(table))), length),
+            ref.dense_attention_fp64(q, *ref.gather_history(sub, layer, list(range(len(table))), length))
+            .reshape(1, 32, 1, 64)
+            .half(),
+        )
+    return out
+
+
+@pytest.mark.parametrize("parts", [4, 16, 32, 128])
+def test_batched_decode_b64_matches_oracle(device, parts):
+    """Batch 64, lengths U{1..2048}, fragmented tables over an 8192-block pool; every row
+    against the oracle restatement and FP64, for several split-K partition sizes."""
+    _say("batched b64 parts", parts)
+    w = workloads.batched_decode(batch=64, num_blocks=8192)
+    pool = _random_pool(device, w.num_blocks, 11)
+    layer = 5
+    queries = torch.from_numpy(w.queries(layer)).to(device)
+    out = torch.empty_like(queries)
+    _hip.paged_decode_attention(
+        out, queries, pool, layer, torch.from_numpy(w.tables).to(device), torch.from_numpy(w.lengths).to(device),
+        partition_blocks=parts,
+    )
+    torch.cuda.synchronize()
+    expected = _oracle_rows(pool, layer, w, queries, range(w.batch))
+    for b, (oracle, fp64) in expected.items():
+        got = out[b : b + 1].reshape(1, 32, 1, 64).cpu()
+        torch.testing.assert_close(got, oracle, **TOL, msg=lambda m: f"row {b} len {w.lengths[b]}: {m}")
+        torch.testing.assert_close(got, fp64, **TOL, msg=lambda m: f"row {b} len {w.lengths[b]} fp64: {m}")
+
+
+def test_long_context_b256_full_length(device):
+    """Batch 256 at 2048 tokens (128 blocks each) over a fully shuffled 40000-block pool:
+    rows against the oracle, and every partition size giving the same answer."""
+    _say("b256 long context")
+    w = workloads.batched_decode(batch=256, num_blocks=40000, fixed_length=2048, seed=44)
+    pool = _random_pool(device, w.num_blocks, 12)
+    layer = 21
+    queries = torch.from_numpy(w.queries(layer)).to(device)
+    tables = torch.from_numpy(w.tables).to(device)
+    lens = torch.from_numpy(w.lengths).to(device)
+    results = {}
+    for parts in (8, 32, 128):
+        out = torch.empty_like(queries)
+        _hip.paged_decode_attention(out, queries, pool, layer, tables, lens, partition_blocks=parts)
+        results[parts] = out
+    torch.cuda.synchronize()
+    for parts in (8, 128):
+        torch.testing.assert_close(results[parts], results[32], **TOL)
+    expected = _oracle_rows(pool, layer, w, queries, [0, 1, 127, 255])
+    for b, (oracle, fp64) in expected.items():
+        got = results[32][b : b + 1].reshape(1, 32, 1, 64).cpu()
+        torch.testing.assert_close(got, oracle, **TOL)
+        torch.testing.assert_close(got, fp64, **TOL)
+
+
+def test_constant_values_return_the_constant(device):
+    """Size-independent property at full batch: V == c everywhere gives c for any scores."""
+    w = workloads.batched_decode(batch=64, num_blocks=8192, seed=45)
+    pool = _random_pool(device, w.num_blocks, 13)
+    pool[:, 1] = 0.375
+    queries = torch.from_numpy(w.queries(0)).to(device)
+    out = torch.empty_like(queries)
+    _hip.paged_decode_attention(
+        out, queries, pool, 0, torch.from_numpy(w.tables).to(device), torch.from_numpy(w.lengths).to(device)
+    )
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.full_like(out, 0.375))
+
+
+def test_block_table_indirection_is_invisible(device):
+    """Moving a sequence's blocks to other physical ids (and permuting its table to match)
+    gives bit-identical output."""
+    w = workloads.batched_decode(batch=8, num_blocks=2048, seed=46)
+    pool = _random_pool(device, w.num_blocks, 14)
+    queries = torch.from_numpy(w.queries(3)).to(device)
+    tables = torch.from_numpy(w.tables).to(device)
+    lens = torch.from_numpy(w.lengths).to(device)
+    first = torch.empty_like(queries)
+    _hip.paged_decode_attention(first, queries, pool, 3, tables, lens)
+    perm = torch.randperm(w.num_blocks, device=device)
+    moved = torch.empty_like(pool)
+    moved[:, :, perm] = pool  # block i now lives at perm[i]
+    second = torch.empty_like(queries)
+    _hip.paged_decode_attention(second, queries, moved, 3, perm[tables.long()].int(), lens)
+    torch.cuda.synchronize()
+    assert torch.equal(first, second)
+
+
+def test_out_of_range_block_id_poisons_only_its_row(device):
+    """A table entry outside the pool never reads out of bounds: that row's output is NaN,
+    the other rows are unaffected."""
+    w = workloads.batched_decode(batch=4, num_blocks=512, lo=40, hi=300, seed=47)
+    pool = _random_pool(device, w.num_blocks, 15)
+    queries = torch.from_numpy(w.queries(0)).to(device)
+    tables = torch.from_numpy(w.tables).to(device)
+    lens = torch.from_numpy(w.lengths).to(device)
+    good = torch.empty_like(queries)
+    _hip.paged_decode_attention(good, queries, pool, 0, tables, lens)
+    broken = tables.clone()
+    broken[2, 1] = w.num_blocks + 7
+    bad = torch.empty_like(queries)
+    _hip.paged_decode_attention(bad, queries, pool, 0, broken, lens)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad[2]).all()
+    for b in (0, 1, 3):
+        assert torch.equal(bad[b], good[b])
+
+
+def test_batched_api_matches_single_request_api(device):
+    pool = torch.full((22, 2, 40, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    gen = torch.Generator(device=device).manual_seed(3)
+    requests = []
+    for index, tokens in enumerate((1, 16, 17, 100, 300)):
+        key = torch.randn(22, tokens, 4, 64, dtype=torch.float16, device=device, generator=gen)
+        value = torch.randn(22, tokens, 4, 64, dtype=torch.float16, device=device, generator=gen)
+        request = RequestId(f"r{index}")
+        allocator.create(KVReservation(request, (tokens + 15) // 16))
+        allocator.append(request, key, value)
+        requests.append(request)
+    query = torch.randn(5, 32, 1, 64, dtype=torch.float16, device=device, generator=gen)
+    batched = paged_attention_batch(query, allocator, requests, layer_index=4)
+    for row, request in enumerate(requests):
+        single = paged_attention(query[row : row + 1], allocator, request, layer_index=4)
+        assert torch.equal(single, batched[row : row + 1])
