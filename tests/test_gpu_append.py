@@ -187,7 +187,7 @@ def test_strided_and_misaligned_sources_copy_exactly(device, layout):
 def test_decode_writes_match_the_oracle(device):
     """Staged decode: single-row and batched writes of all 22 layers land exactly where the
     reference's write_decode_layer puts them; the commit publishes the new lengths."""
-    pool = torch.full((22, 2, 8, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    pool = torch.full((22, 2, 9, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
     allocator = KVAllocator(pool)
     requests = (RequestId("p"), RequestId("q"), RequestId("r"))
     lengths = {"p": 16, "q": 5, "r": 32}
@@ -205,7 +205,7 @@ def test_decode_writes_match_the_oracle(device):
             else:
                 for row, request in enumerate(requests):
                     allocator.write_decode_layer(request, layer, step_key[layer, row], step_value[layer, row])
-    lifo = ref.LifoFreeList.fresh(8)
+    lifo = ref.LifoFreeList.fresh(9)
     for request in requests:
         lifo.grow_to(request, lengths[request])
     tables = lifo.decode_step({request: lengths[request] for request in requests})
