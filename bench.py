@@ -4,7 +4,8 @@ Workload (the metric's configuration): batched one-token paged decode attention,
 32 query / 4 KV heads, head dim 64, fp16 KV with N(0,1) values, context lengths drawn
 uniformly from 1..2048 (partial last blocks included), fragmented block tables carved from
 a random permutation of an 8192-block pool, repeated over the pool's 22 layers. A step is
-one pass over the 22 layers (partition kernel + split-K reduce per layer), with inputs
+one pass over the 22 layers (one attention launch per layer; split-K partitions are
+merged inside the same launch), with inputs
 resident in HBM; the 22 layer planes (1.48 GB of KV per step) exceed the 256 MB Infinity
 Cache, so the bytes come from HBM.
 
@@ -52,7 +53,14 @@ def attention_bytes(lengths: np.ndarray) -> int:
 class DecodeLayers:
     """Device buffers and raw C-ABI launches for the 22-layer decode step."""
 
-    def __init__(self, w: workloads.BatchedDecode, device: torch.device, partition_blocks: int, seed: int) -> None:
+    def __init__(
+        self,
+        w: workloads.BatchedDecode,
+        device: torch.device,
+        partition_blocks: int,
+        seed: int,
+        separate_reduce: bool = _hip.DEFAULT_SEPARATE_REDUCE,
+    ) -> None:
         gen = torch.Generator(device=device).manual_seed(seed)
         self.w = w
         self.device = device
@@ -62,124 +70,64 @@ class DecodeLayers:
         self.tables = torch.from_numpy(w.tables).to(device)
         self.lens = torch.from_numpy(w.lengths).to(device)
         self.parts = partition_blocks
+        self.flags = _hip.SEPARATE_REDUCE if separate_reduce else 0
         self.lib = _hip.load()
-        max_blocks = int(w.tables.shape[1])
-        floats = int(self.lib.pc_attn_workspace_floats(w.batch, max_blocks, partition_blocks))
-        self.workspace = torch.empty(floats, dtype=torch.float32, device=device)
-        max_parts = (max_blocks + partition_blocks - 1) // partition_blocks
-        self.ws_out = self.workspace.data_ptr()
-        self.ws_ml = self.ws_out + w.batch * 32 * max_parts * 64 * 4
-        self.max_blocks = max_blocks
+        self.max_blocks = int(w.tables.shape[1])
+        nbytes = int(self.lib.pc_attn_workspace_bytes(w.batch, self.max_blocks, partition_blocks))
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        self.tickets = torch.zeros(w.batch * 4, dtype=torch.int32, device=device)
+        # One decode plan per step, shared by the 22 layers (built from the host lengths,
+        # like the block tables).
+        self.items = torch.from_numpy(_hip.plan_work_items(w.lengths, self.max_blocks, partition_blocks)).to(device)
 
-    def _args(self, layer: int, stream: int):
-        return (
+    def launch(self, layer: int, stream: int) -> None:
+        status = self.lib.pc_paged_decode_attn(
             self.out[layer].data_ptr(), self.queries[layer].data_ptr(), self.pool.data_ptr(), self.w.num_blocks,
             layer, self.tables.data_ptr(), self.max_blocks, self.lens.data_ptr(), self.w.batch, self.parts,
-            self.ws_out, self.ws_ml, stream,
+            self.items.data_ptr(), self.items.shape[0], self.workspace.data_ptr(), self.tickets.data_ptr(),
+            self.flags, stream,
         )
+        if status:
+            raise RuntimeError(self.lib.pc_last_error().decode())
 
     def step(self) -> None:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         for layer in range(LAYERS):
-            status = self.lib.pc_paged_decode_attn(*self._args(layer, stream))
-            if status:
-                raise RuntimeError(self.lib.pc_last_error().decode())
+            self.launch(layer, stream)
 
-    def timed_kernels(self, steps: int) -> tuple[float, float]:
-        """Mean duration (ms) of the partition kernel and of the reduce kernel, from HIP
-        events recorded around each launch on the launch stream."""
+    def timed_launches(self, steps: int) -> float:
+        """Mean duration (ms) of one layer's attention launch, from HIP events recorded
+        around each launch on the launch stream."""
         stream = torch.cuda.current_stream(self.device)
         handle = stream.cuda_stream
-        part_ms, red_ms = [], []
+        times = []
         for _ in range(steps):
             marks = []
             for layer in range(LAYERS):
-                e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record(stream)
-                self.lib.pc_paged_decode_attn_partitions(*self._args(layer, handle))
+                self.launch(layer, handle)
                 e1.record(stream)
-                self.lib.pc_paged_decode_attn_reduce(
-                    self.out[layer].data_ptr(), self.lens.data_ptr(), self.w.batch, self.max_blocks, self.parts,
-                    self.ws_out, self.ws_ml, handle,
-                )
-                e2.record(stream)
-                marks.append((e0, e1, e2))
+                marks.append((e0, e1))
             torch.cuda.synchronize(self.device)
-            for e0, e1, e2 in marks:
-                part_ms.append(e0.elapsed_time(e1))
-                red_ms.append(e1.elapsed_time(e2))
-        return float(np.mean(part_ms)), float(np.mean(red_ms))
+            times.extend(e0.elapsed_time(e1) for e0, e1 in marks)
+        return float(np.mean(times))
 
 
-def cpu_baseline(layers: DecodeLayers, seconds: float) -> dict:
-    """The oracle's restatement of the reference torch CPU path (attention.py:14-53), run
-    row by row on layer 0 until ~`seconds` of CPU work, on all of this host's cores."""
-    from oracle import paged_reference as ref
-
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    w = layers.w
-    layer = 0
-    done_bytes, done_rows, elapsed = 0, 0, 0.0
-    order = np.random.Generator(np.random.PCG64(5)).permutation(w.batch)
-    for b in order:
-        length = int(w.lengths[b])
-        table = w.tables[b, : (length + 15) // 16]
-        blocks = torch.from_numpy(table.astype(np.int64)).to(layers.device)
-        sub = torch.empty((LAYERS, 2, len(table), 16, 4, 64), dtype=torch.float16)
-        sub[layer] = layers.pool[layer].index_select(1, blocks).cpu()
-        query = layers.queries[layer, b].reshape(1, 32, 1, 64).cpu()
-        start = time.perf_counter()
-        ref.reference_paged_attention(query, sub, layer, list(range(len(table))), length)
-        elapsed += time.perf_counter() - start
-        done_bytes += attention_bytes(np.array([length], dtype=np.int32))
-        done_rows += 1
-        if elapsed >= seconds:
-            break
-    return {
-        "value": round(done_bytes / elapsed / 1e9, 4),
-        "unit": "GB/s",
-        "cores": cores,
-        "kind": "port",
-        "sample": f"{done_rows} of {w.batch} sequences of layer 0 (sum of lengths "
-        f"{int(sum(int(w.lengths[b]) for b in order[:done_rows]))} tokens), one reference paged_attention call each, "
-        f"{elapsed:.1f} s; tok/s equivalent {done_rows / elapsed / LAYERS:.2f}",
-    }
-
-
-def main() -> int:
-    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=50)
-    parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--partition-blocks", type=int, default=None)
-    parser.add_argument("--cpu-seconds", type=float, default=15.0)
-    parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--no-graph", action="store_true", help="launch from Python instead of replaying a HIP graph")
-    args = parser.parse_args()
-    if args.gpus != 1:
-        print(
-            f"bench.py measures one GPU: the paged decode path is per-GPU (sequences shard across "
-            f"GPUs with no exchange), so --gpus {args.gpus} is not run",
-            file=sys.stderr,
-        )
-        return 2
-
+def run_decode(
+    steps: int, warmup: int, partition_blocks: int, use_graph: bool = True,
+    separate_reduce: bool = _hip.DEFAULT_SEPARATE_REDUCE,
+) -> dict:
+    """Times `steps` 22-layer decode steps of the batch-64 workload; returns the figures."""
     device = torch.device("cuda:0")
-    torch.cuda.set_device(device)
-    parts = args.partition_blocks or _hip.default_partition_blocks()
     w = workloads.batched_decode(batch=64, num_blocks=8192)
-    layers = DecodeLayers(w, device, parts, seed=1234)
+    layers = DecodeLayers(w, device, partition_blocks, seed=1234, separate_reduce=separate_reduce)
     bytes_per_launch = attention_bytes(w.lengths)
-    bytes_per_step = bytes_per_launch * LAYERS
-    print(f"workload: batch {w.batch}, sum of lengths {int(w.lengths.sum())}, {bytes_per_launch / 1e6:.1f} MB per layer", file=sys.stderr, flush=True)
-
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         layers.step()
     torch.cuda.synchronize(device)
     eager_out = layers.out.clone()
 
-    use_graph = not args.no_graph
     replay = layers.step
     if use_graph:
         side = torch.cuda.Stream(device=device)
@@ -204,22 +152,94 @@ def main() -> int:
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         replay()
     stop.record()
     torch.cuda.synchronize(device)
     total_ms = start.elapsed_time(stop)
     if not torch.equal(layers.out, eager_out):
         raise RuntimeError("timed steps produced different outputs than the warmup")
-    ms_per_step = total_ms / args.steps
-    gbps = bytes_per_step * args.steps / (total_ms / 1e3) / 1e9
-    tokens_per_s = w.batch * args.steps / (total_ms / 1e3)
+    launch_ms = layers.timed_launches(steps=5)
+    return {
+        "layers": layers,
+        "w": w,
+        "bytes_per_launch": bytes_per_launch,
+        "total_ms": total_ms,
+        "ms_per_step": total_ms / steps,
+        "gbps": bytes_per_launch * LAYERS * steps / (total_ms / 1e3) / 1e9,
+        "tokens_per_s": w.batch * steps / (total_ms / 1e3),
+        "launch_ms": launch_ms,
+        "launch_gbps": bytes_per_launch / (launch_ms / 1e3) / 1e9,
+        "graph": use_graph,
+    }
 
-    part_ms, red_ms = layers.timed_kernels(steps=5)
-    achieved = bytes_per_launch / (part_ms / 1e3) / 1e9
+
+def cpu_baseline(layers: DecodeLayers, seconds: float) -> dict:
+    """The oracle's op-for-op restatement of the reference torch CPU path
+    (attention.py:14-53, one call per sequence as in decoder.py:182-190), run over whole
+    layers of the same workload until ~`seconds` of CPU work, on all of this host's cores.
+    Only the attention calls are timed (copying each layer's blocks to host memory is not)."""
+    from oracle import paged_reference as ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    w = layers.w
+    host_tables = [w.tables[b, : (int(w.lengths[b]) + 15) // 16].tolist() for b in range(w.batch)]
+    done_bytes, done_layers, elapsed = 0, 0, 0.0
+    for layer in range(LAYERS):
+        used = sorted({blk for table in host_tables for blk in table})
+        remap = {blk: i for i, blk in enumerate(used)}
+        index = torch.tensor(used, dtype=torch.long, device=layers.device)
+        sub = torch.empty((LAYERS, 2, len(used), 16, 4, 64), dtype=torch.float16)
+        sub[layer] = layers.pool[layer].index_select(1, index).cpu()
+        queries = layers.queries[layer].reshape(w.batch, 1, 32, 1, 64).cpu()
+        start = time.perf_counter()
+        for b in range(w.batch):
+            ref.reference_paged_attention(queries[b], sub, layer, [remap[x] for x in host_tables[b]], int(w.lengths[b]))
+        elapsed += time.perf_counter() - start
+        done_bytes += attention_bytes(w.lengths)
+        done_layers += 1
+        if elapsed >= seconds:
+            break
+    return {
+        "value": round(done_bytes / elapsed / 1e9, 4),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{done_layers} of 22 layers x all {w.batch} sequences of the same workload, one reference "
+        f"paged_attention call per sequence, {elapsed:.1f} s of CPU time; decode tokens/s at that rate "
+        f"{w.batch * done_layers / LAYERS / elapsed:.2f}",
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--partition-blocks", type=int, default=None)
+    parser.add_argument("--merge", choices=("separate", "fused"), default="separate" if _hip.DEFAULT_SEPARATE_REDUCE else "fused",
+                        help="merge split-K partitions in a second kernel or in the last partition wave")
+    parser.add_argument("--cpu-seconds", type=float, default=15.0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-graph", action="store_true", help="launch from Python instead of replaying a HIP graph")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU: the paged decode path is per-GPU (sequences shard across "
+            f"GPUs with no exchange), so --gpus {args.gpus} is not run",
+            file=sys.stderr,
+        )
+        return 2
+
+    torch.cuda.set_device(0)
+    parts = args.partition_blocks or _hip.default_partition_blocks()
+    r = run_decode(args.steps, args.warmup, parts, use_graph=not args.no_graph, separate_reduce=args.merge == "separate")
+    w, layers = r["w"], r["layers"]
     print(
-        f"step {ms_per_step:.3f} ms ({'graph' if use_graph else 'eager'}), {gbps:.0f} GB/s, {tokens_per_s:.0f} tok/s; "
-        f"partition kernel {part_ms * 1e3:.1f} us ({achieved:.0f} GB/s), reduce {red_ms * 1e3:.1f} us",
+        f"workload: batch {w.batch}, sum of lengths {int(w.lengths.sum())}, {r['bytes_per_launch'] / 1e6:.1f} MB per layer; "
+        f"step {r['ms_per_step']:.3f} ms ({'graph' if r['graph'] else 'eager'}), {r['gbps']:.0f} GB/s, "
+        f"{r['tokens_per_s']:.0f} tok/s; one layer's launch {r['launch_ms'] * 1e3:.1f} us ({r['launch_gbps']:.0f} GB/s)",
         file=sys.stderr,
         flush=True,
     )
@@ -230,12 +250,12 @@ def main() -> int:
 
     record = {
         "metric": "paged-decode attn HBM GB/s (% of ~8 TB/s peak) + decode tok/s, batch 64 ctx<=2048",
-        "value": round(gbps, 2),
+        "value": round(r["gbps"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(r["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -249,22 +269,23 @@ def main() -> int:
             "pool_blocks": w.num_blocks,
             "sum_context_tokens": int(w.lengths.sum()),
             "partition_blocks": parts,
+            "split_k_merge": "separate_kernel" if args.merge == "separate" else "fused_last_arriver",
             "kv_dtype": "f16",
-            "launch": "hip_graph" if use_graph else "eager",
+            "launch": "hip_graph" if r["graph"] else "eager",
         },
-        "hbm_fraction": round(gbps / PEAK_HBM_GBPS, 4),
-        "decode_tokens_per_s": round(tokens_per_s, 1),
+        "hbm_fraction": round(r["gbps"] / PEAK_HBM_GBPS, 4),
+        "decode_tokens_per_s": round(r["tokens_per_s"], 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode_partition_kernel",
-            "achieved": round(achieved, 2),
+            "kernel": "pc_paged_decode_attn: paged_decode_partition_kernel"
+            + (" + paged_decode_reduce_kernel" if args.merge == "separate" else " (fused merge)"),
+            "achieved": round(r["launch_gbps"], 2),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "frac": round(r["launch_gbps"] / PEAK_HBM_GBPS, 4),
             "traffic": None,
-            "avg_launch_us": round(part_ms * 1e3, 3),
-            "bytes_per_launch": bytes_per_launch,
-            "reduce_avg_launch_us": round(red_ms * 1e3, 3),
+            "avg_launch_us": round(r["launch_ms"] * 1e3, 3),
+            "bytes_per_launch": r["bytes_per_launch"],
         },
         "cpu_baseline": baseline,
     }

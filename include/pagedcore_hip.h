@@ -69,41 +69,59 @@ int pc_kv_append(void* pool, int64_t num_blocks, int32_t layer_begin, int32_t nu
  * block table is walked inside the kernel.
  *
  *   query        [batch][32][64] fp16, contiguous; q head h reads kv head h / 8
- *   out          [batch][32][64] fp16, contiguous
+ *   out          [batch][32][64] fp16, contiguous, 16-byte aligned (query and pool too)
  *   block_tables [batch][max_blocks] int32 physical block ids (row b lists sequence b's
  *                blocks in logical order; only the first ceil(len/16) are read)
  *   context_lens [batch] int32, each in [1, max_blocks * 16]
  *   out[b][h] = softmax(q[b][h] . K[b][:len]^T / 8) . V[b][:len], computed in fp32 and
  *   rounded once to fp16. Slots past len are never multiplied, so poisoned (NaN) tail
- *   slots do not reach the output.
+ *   slots do not reach the output. A block id outside [0, num_blocks) is never
+ *   dereferenced; its sequence's output rows become NaN.
  *
- * Long contexts are split into partitions of `partition_blocks` blocks (a multiple of 4,
- * 4..128); partials go to the fp32 workspace and a second kernel merges them. Workspace:
- *   ws_out [batch][32][max_partitions][64] fp32, ws_ml [batch][32][max_partitions][2] fp32,
- *   max_partitions = ceil(max_blocks / partition_blocks)  (see pc_attn_workspace_floats).
- * The workspace is scratch: no contents need to survive between calls.
+ * Long contexts are split into partitions of `partition_blocks` blocks (1..64), one wave
+ * per (partition, kv head). By default the last wave to finish a (sequence, kv head)
+ * merges that sequence's partitions (one launch); flags = PC_ATTN_SEPARATE_REDUCE merges
+ * them in a second kernel instead.
+ *   work_items  null: the grid covers batch * ceil(max_blocks / partition_blocks)
+ *               partition slots and the slots past a sequence's length exit at once;
+ *               otherwise the host-built plan from pc_attn_plan() for the same
+ *               context_lens, block_tables width and partition_blocks (device int32
+ *               pairs, num_work_items of them): the grid then holds only partitions
+ *               that exist. A plan that does not match context_lens leaves rows unwritten.
+ *               One plan serves every layer of a decode step.
+ *   workspace  fp32 partials, pc_attn_workspace_bytes() bytes, 256-byte aligned; scratch,
+ *              nothing in it needs to survive between calls (unused when no sequence
+ *              needs more than one partition);
+ *   tickets    int32 [batch * 4], one merge ticket per (sequence, kv head), only read by
+ *              the fused merge: ZERO-FILLED BEFORE ITS FIRST USE; every call leaves the
+ *              tickets at zero again, so one ticket array serves any number of later calls.
+ * Calls that share a workspace or tickets must not overlap (use one set per stream).
  */
+#define PC_ATTN_SEPARATE_REDUCE 1
+
 int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t num_blocks,
                          int32_t layer, const int32_t* block_tables, int32_t max_blocks,
                          const int32_t* context_lens, int32_t batch, int32_t partition_blocks,
-                         float* ws_out, float* ws_ml, void* stream);
+                         const int32_t* work_items, int32_t num_work_items, void* workspace,
+                         int32_t* tickets, int32_t flags, void* stream);
 
-/* The two kernels of pc_paged_decode_attn, launched separately (same arguments). The
- * partition kernel writes `out` directly for sequences that fit in one partition; the
- * reduce kernel merges the others. Exposed so callers can time or order them apart. */
-int pc_paged_decode_attn_partitions(void* out, const void* query, const void* pool,
-                                    int64_t num_blocks, int32_t layer,
-                                    const int32_t* block_tables, int32_t max_blocks,
-                                    const int32_t* context_lens, int32_t batch,
-                                    int32_t partition_blocks, float* ws_out, float* ws_ml,
-                                    void* stream);
-int pc_paged_decode_attn_reduce(void* out, const int32_t* context_lens, int32_t batch,
-                                int32_t max_blocks, int32_t partition_blocks,
-                                const float* ws_out, const float* ws_ml, void* stream);
+/* Workspace size in bytes for pc_paged_decode_attn; 0 on invalid arguments. */
+int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t partition_blocks);
 
-/* Workspace size in floats for ws_out + ws_ml together (ws_ml starts after ws_out,
- * at offset batch * 32 * max_partitions * 64); 0 on invalid arguments. */
-int64_t pc_attn_workspace_floats(int32_t batch, int32_t max_blocks, int32_t partition_blocks);
+/*
+ * Host-side decode plan (no device access). context_lens and work_items are HOST
+ * memory here. Writes one (sequence, partition) int32 pair per partition that exists,
+ * sequence-major, and returns how many; returns -pc_status on invalid arguments or if
+ * `capacity` (in pairs) is too small. pc_attn_plan_capacity() gives a capacity that
+ * always suffices (-1 on invalid arguments).
+ *
+ * Replaces nothing in the reference: PagedCore walks each sequence's pages in Python
+ * (reference src/pagedcore/attention.py:31-53); the plan is what lets one launch cover a
+ * ragged batch without idle waves.
+ */
+int32_t pc_attn_plan(const int32_t* context_lens, int32_t batch, int32_t max_blocks,
+                     int32_t partition_blocks, int32_t* work_items, int64_t capacity);
+int64_t pc_attn_plan_capacity(int32_t batch, int32_t max_blocks, int32_t partition_blocks);
 
 /* Default partition size (blocks) used by the Python layer. */
 int32_t pc_attn_default_partition_blocks(void);

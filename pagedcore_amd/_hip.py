@@ -13,10 +13,11 @@ import os
 import threading
 from typing import Dict, Optional, Tuple
 
+import numpy as np
 import torch
 from torch import Tensor
 
-ABI_VERSION = 1
+ABI_VERSION = 5
 LIBRARY_NAME = "libpagedcore_hip.so"
 
 _lock = threading.Lock()
@@ -42,17 +43,16 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pc_last_error.argtypes = []
     lib.pc_attn_default_partition_blocks.restype = _i32
     lib.pc_attn_default_partition_blocks.argtypes = []
-    lib.pc_attn_workspace_floats.restype = _i64
-    lib.pc_attn_workspace_floats.argtypes = [_i32, _i32, _i32]
+    lib.pc_attn_workspace_bytes.restype = _i64
+    lib.pc_attn_workspace_bytes.argtypes = [_i32, _i32, _i32]
     lib.pc_kv_append.restype = ctypes.c_int
     lib.pc_kv_append.argtypes = [_p, _i64, _i32, _i32, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _p]
-    attn = [_p, _p, _p, _i64, _i32, _p, _i32, _p, _i32, _i32, _p, _p, _p]
-    for name in ("pc_paged_decode_attn", "pc_paged_decode_attn_partitions"):
-        fn = getattr(lib, name)
-        fn.restype = ctypes.c_int
-        fn.argtypes = attn
-    lib.pc_paged_decode_attn_reduce.restype = ctypes.c_int
-    lib.pc_paged_decode_attn_reduce.argtypes = [_p, _p, _i32, _i32, _i32, _p, _p, _p]
+    lib.pc_paged_decode_attn.restype = ctypes.c_int
+    lib.pc_paged_decode_attn.argtypes = [_p, _p, _p, _i64, _i32, _p, _i32, _p, _i32, _i32, _p, _i32, _p, _p, _i32, _p]
+    lib.pc_attn_plan.restype = _i32
+    lib.pc_attn_plan.argtypes = [_p, _i32, _i32, _i32, _p, _i64]
+    lib.pc_attn_plan_capacity.restype = _i64
+    lib.pc_attn_plan_capacity.argtypes = [_i32, _i32, _i32]
 
 
 def load() -> ctypes.CDLL:
@@ -126,20 +126,65 @@ def kv_append(pool: Tensor, layer_begin: int, key: Tensor, value: Tensor, slot_m
     _check(lib, "pc_kv_append", status)
 
 
+SEPARATE_REDUCE = 1  # PC_ATTN_SEPARATE_REDUCE
+# Split-K partitions are merged by the separate merge kernel unless a caller asks for
+# the fused last-arriver merge: on MI355X the second launch costs less than making every
+# partition wave wait for its stores to be acknowledged before it takes a ticket.
+DEFAULT_SEPARATE_REDUCE = True
+
 _workspaces: Dict[Tuple[int, int], Tensor] = {}
+_tickets: Dict[Tuple[int, int], Tensor] = {}
 
 
-def attention_workspace(device: torch.device, floats: int) -> Tensor:
-    """Split-K scratch for the current stream of `device`, grown on demand and reused.
+def _stream_key(device: torch.device) -> Tuple[int, int]:
+    return (device.index if device.index is not None else torch.cuda.current_device(), _stream(device))
+
+
+def attention_workspace(device: torch.device, nbytes: int) -> Tensor:
+    """Split-K partial scratch for the current stream of `device`, grown on demand.
 
     Reuse is safe because every call that uses it is ordered on that one stream.
     """
-    key = (device.index if device.index is not None else torch.cuda.current_device(), _stream(device))
+    key = _stream_key(device)
     workspace = _workspaces.get(key)
-    if workspace is None or workspace.numel() < floats:
-        workspace = torch.empty(max(floats, 1), dtype=torch.float32, device=device)
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
         _workspaces[key] = workspace
     return workspace
+
+
+def merge_tickets(device: torch.device, batch: int) -> Tensor:
+    """Merge tickets (int32, one per sequence and kv head) for the current stream.
+
+    Zero-filled when created or grown; the kernel leaves every ticket at zero after each
+    call, so the array is reused as is.
+    """
+    key = _stream_key(device)
+    tickets = _tickets.get(key)
+    if tickets is None or tickets.numel() < batch * 4:
+        tickets = torch.zeros(max(batch * 4, 64), dtype=torch.int32, device=device)
+        _tickets[key] = tickets
+    return tickets
+
+
+def workspace_bytes(batch: int, max_blocks: int, partition_blocks: int) -> int:
+    return int(load().pc_attn_workspace_bytes(batch, max_blocks, partition_blocks))
+
+
+def plan_work_items(context_lens: np.ndarray, max_blocks: int, partition_blocks: int) -> np.ndarray:
+    """Host decode plan: int32 [items, 2] (sequence, partition) rows for every partition
+    that exists, computed by pc_attn_plan from host context lengths."""
+    lib = load()
+    lens = np.ascontiguousarray(context_lens, dtype=np.int32)
+    batch = int(lens.shape[0])
+    capacity = int(lib.pc_attn_plan_capacity(batch, max_blocks, partition_blocks))
+    if capacity < 0:
+        _check(lib, "pc_attn_plan_capacity", 1)
+    items = np.empty((max(capacity, 1), 2), dtype=np.int32)
+    count = int(lib.pc_attn_plan(lens.ctypes.data, batch, max_blocks, partition_blocks, items.ctypes.data, capacity))
+    if count < 0:
+        _check(lib, "pc_attn_plan", -count)
+    return items[:count]
 
 
 def paged_decode_attention(
@@ -151,26 +196,41 @@ def paged_decode_attention(
     context_lens: Tensor,
     *,
     partition_blocks: Optional[int] = None,
+    work_items: Optional[Tensor] = None,
     workspace: Optional[Tensor] = None,
+    tickets: Optional[Tensor] = None,
+    separate_reduce: Optional[bool] = None,
 ) -> None:
     """out[b] = paged decode attention of query[b] over layer `layer` of the pool.
 
     out/query: fp16 [batch, 32, 64] contiguous; block_tables: int32 [batch, max_blocks]
-    contiguous; context_lens: int32 [batch]. All on the pool's device.
+    contiguous; context_lens: int32 [batch]. All on the pool's device. `work_items`: the
+    plan_work_items() rows for the same lengths, table width and partition size, as a
+    contiguous int32 device tensor (None: full grid). `workspace` (uint8) and `tickets`
+    (int32 [>= batch*4], zero-filled before first use) default to per-stream cached
+    buffers. `separate_reduce` None: DEFAULT_SEPARATE_REDUCE.
     """
+    if separate_reduce is None:
+        separate_reduce = DEFAULT_SEPARATE_REDUCE
     lib = load()
     batch, max_blocks = block_tables.shape
     parts = partition_blocks if partition_blocks is not None else default_partition_blocks()
-    floats = int(lib.pc_attn_workspace_floats(batch, max_blocks, parts))
-    if floats <= 0:
+    nbytes = int(lib.pc_attn_workspace_bytes(batch, max_blocks, parts))
+    if nbytes <= 0:
         raise HipExtensionError(f"invalid attention shape batch={batch} max_blocks={max_blocks} partition={parts}")
     if workspace is None:
-        workspace = attention_workspace(pool.device, floats)
-    elif workspace.numel() < floats or workspace.dtype != torch.float32:
-        raise HipExtensionError(f"workspace needs {floats} fp32 elements")
-    max_parts = (max_blocks + parts - 1) // parts
-    ws_out = workspace.data_ptr()
-    ws_ml = ws_out + batch * 32 * max_parts * 64 * 4
+        workspace = attention_workspace(pool.device, nbytes)
+    elif workspace.numel() * workspace.element_size() < nbytes:
+        raise HipExtensionError(f"workspace needs {nbytes} bytes")
+    if tickets is None:
+        tickets = merge_tickets(pool.device, batch)
+    elif tickets.dtype != torch.int32 or tickets.numel() < batch * 4:
+        raise HipExtensionError(f"tickets must be int32 with at least {batch * 4} entries")
+    if work_items is not None and (
+        work_items.dtype != torch.int32 or work_items.dim() != 2 or work_items.shape[1] != 2
+        or not work_items.is_contiguous()
+    ):
+        raise HipExtensionError("work_items must be a contiguous int32 [items, 2] tensor")
     status = lib.pc_paged_decode_attn(
         out.data_ptr(),
         query.data_ptr(),
@@ -182,8 +242,11 @@ def paged_decode_attention(
         context_lens.data_ptr(),
         batch,
         parts,
-        ws_out,
-        ws_ml,
+        work_items.data_ptr() if work_items is not None else None,
+        int(work_items.shape[0]) if work_items is not None else 0,
+        workspace.data_ptr(),
+        tickets.data_ptr(),
+        SEPARATE_REDUCE if separate_reduce else 0,
         _stream(pool.device),
     )
     _check(lib, "pc_paged_decode_attn", status)

@@ -51,8 +51,10 @@ def _launch(
     if not q.is_contiguous():
         q = q.contiguous()
     out = torch.empty((batch, Q_HEADS, 1, HEAD_DIM), dtype=torch.float16, device=query.device)
+    parts = partition_blocks if partition_blocks is not None else _hip.default_partition_blocks()
+    items = allocator.decode_work_items(request_ids, layer_index=layer_index, partition_blocks=parts)
     _hip.paged_decode_attention(
-        out, q, pool, layer_index, tables, lengths, partition_blocks=partition_blocks
+        out, q, pool, layer_index, tables, lengths, partition_blocks=parts, work_items=items
     )
     return out
 

@@ -106,6 +106,17 @@ class _HostOnlyWriter:
         )
 
 
+@dataclass(slots=True)
+class _DecodeBatch:
+    """Device block tables and lengths of one batch of requests, plus the host lengths
+    and the per-partition-size decode plans built from them."""
+
+    tables: Tensor
+    lengths: Tensor
+    host_lengths: np.ndarray
+    plans: Dict[int, Tensor]
+
+
 @dataclass(frozen=True, slots=True)
 class _SequenceCache:
     reservation: KVReservation
@@ -159,7 +170,7 @@ class KVAllocator:
         self._decode_appends: Optional[Dict[RequestId, _TokenAppend]] = None
         # Bumped whenever a table or length may change; keys the device-table cache.
         self._version = 0
-        self._table_cache: Dict[tuple, Tuple[Tensor, Tensor]] = {}
+        self._table_cache: Dict[tuple, _DecodeBatch] = {}
         self._decode_slot_cache: Dict[Tuple[RequestId, ...], Tensor] = {}
 
     @property
@@ -413,6 +424,24 @@ class KVAllocator:
         requests whose staged layer is written); W is the longest table in the batch.
         Cached per allocator state, so the 22 layers of a decode step share one upload.
         """
+        batch = self._gather(request_ids, layer_index)
+        return batch.tables, batch.lengths
+
+    def decode_work_items(
+        self, request_ids: Sequence[RequestId], *, layer_index: int, partition_blocks: int
+    ) -> Tensor:
+        """Device decode plan (int32 [items, 2] (row, partition) pairs) for the batch that
+        gather_block_tables returns, built once per allocator state and partition size
+        from the host lengths, so the 22 layers of a decode step share it."""
+        batch = self._gather(request_ids, layer_index)
+        items = batch.plans.get(partition_blocks)
+        if items is None:
+            plan = _hip.plan_work_items(batch.host_lengths, int(batch.tables.shape[1]), partition_blocks)
+            items = torch.from_numpy(plan).to(self._pool.device)
+            batch.plans[partition_blocks] = items
+        return items
+
+    def _gather(self, request_ids: Sequence[RequestId], layer_index: int) -> _DecodeBatch:
         if not request_ids:
             raise ValueError("attention requires at least one request")
         self._check_worker()
@@ -431,9 +460,11 @@ class KVAllocator:
         for row, sequence in enumerate(sequences):
             tables[row, : len(sequence.blocks)] = sequence.blocks
             lengths[row] = sequence.length
-        result = (
+        result = _DecodeBatch(
             torch.from_numpy(tables).to(self._pool.device),
             torch.from_numpy(lengths).to(self._pool.device),
+            lengths,
+            {},
         )
         if len(self._table_cache) > 64:
             self._table_cache.clear()

@@ -238,7 +238,7 @@ def _oracle_rows(pool, layer, w, queries, rows):
     return out
 
 
-@pytest.mark.parametrize("parts", [4, 16, 32, 128])
+@pytest.mark.parametrize("parts", [1, 5, 16, 32, 64])
 def test_batched_decode_b64_matches_oracle(device, parts):
     """Batch 64, lengths U{1..2048}, fragmented tables over an 8192-block pool; every row
     against the oracle restatement and FP64, for several split-K partition sizes."""
@@ -271,18 +271,113 @@ def test_long_context_b256_full_length(device):
     tables = torch.from_numpy(w.tables).to(device)
     lens = torch.from_numpy(w.lengths).to(device)
     results = {}
-    for parts in (8, 32, 128):
+    for parts in (8, 32, 64):
         out = torch.empty_like(queries)
         _hip.paged_decode_attention(out, queries, pool, layer, tables, lens, partition_blocks=parts)
         results[parts] = out
     torch.cuda.synchronize()
-    for parts in (8, 128):
+    for parts in (8, 64):
         torch.testing.assert_close(results[parts], results[32], **TOL)
     expected = _oracle_rows(pool, layer, w, queries, [0, 1, 127, 255])
     for b, (oracle, fp64) in expected.items():
         got = results[32][b : b + 1].reshape(1, 32, 1, 64).cpu()
         torch.testing.assert_close(got, oracle, **TOL)
         torch.testing.assert_close(got, fp64, **TOL)
+
+
+def test_fused_merge_equals_separate_reduce_and_rearms_tickets(device):
+    """The last-arriver merge inside the partition kernel gives bit-identical output to the
+    separate reduce kernel, on every call (the tickets return to zero), including inside a
+    replayed HIP graph."""
+    w = workloads.batched_decode(batch=64, num_blocks=8192, seed=48)
+    pool = _random_pool(device, w.num_blocks, 16)
+    queries = torch.from_numpy(w.queries(7)).to(device)
+    tables = torch.from_numpy(w.tables).to(device)
+    lens = torch.from_numpy(w.lengths).to(device)
+    for parts in (3, 8, 32):
+        nbytes = _hip.workspace_bytes(w.batch, tables.shape[1], parts)
+        workspace = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=device)  # scratch: contents irrelevant
+        tickets = torch.zeros(w.batch * 4, dtype=torch.int32, device=device)
+        separate = torch.empty_like(queries)
+        _hip.paged_decode_attention(separate, queries, pool, 7, tables, lens, partition_blocks=parts, workspace=workspace, tickets=tickets, separate_reduce=True)
+        for _ in range(3):
+            fused = torch.full_like(queries, float("nan"))
+            _hip.paged_decode_attention(fused, queries, pool, 7, tables, lens, partition_blocks=parts, workspace=workspace, tickets=tickets, separate_reduce=False)
+            torch.cuda.synchronize()
+            assert torch.equal(fused, separate), parts
+        assert torch.count_nonzero(tickets) == 0
+        graph_out = torch.empty_like(queries)
+        side = torch.cuda.Stream(device=device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side), torch.cuda.graph(graph, stream=side):
+            _hip.paged_decode_attention(graph_out, queries, pool, 7, tables, lens, partition_blocks=parts, workspace=workspace, tickets=tickets, separate_reduce=False)
+        torch.cuda.current_stream(device).wait_stream(side)
+        for _ in range(3):
+            graph_out.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(graph_out, separate), parts
+        assert torch.count_nonzero(tickets) == 0
+
+
+@pytest.mark.parametrize("separate", [False, True])
+def test_planned_grid_equals_full_grid(device, separate):
+    """The host plan (only partitions that exist) gives bit-identical output to the full
+    partition-slot grid, for ragged lengths with empty-tail rows, several partition
+    sizes, both merge modes, and inside replayed HIP graphs."""
+    _say("planned grid, separate", separate)
+    w = workloads.batched_decode(batch=64, num_blocks=8192, seed=49)
+    lengths = w.lengths.copy()
+    lengths[:4] = [1, 16, 17, 2048]
+    pool = _random_pool(device, w.num_blocks, 18)
+    queries = torch.from_numpy(w.queries(9)).to(device)
+    tables = torch.from_numpy(w.tables).to(device)
+    lens = torch.from_numpy(lengths).to(device)
+    for parts in (1, 4, 16, 64):
+        items = torch.from_numpy(_hip.plan_work_items(lengths, tables.shape[1], parts)).to(device)
+        full = torch.full_like(queries, float("nan"))
+        _hip.paged_decode_attention(full, queries, pool, 9, tables, lens, partition_blocks=parts, separate_reduce=separate)
+        planned = torch.full_like(queries, float("nan"))
+        _hip.paged_decode_attention(planned, queries, pool, 9, tables, lens, partition_blocks=parts, work_items=items, separate_reduce=separate)
+        torch.cuda.synchronize()
+        assert torch.equal(planned, full), parts
+        assert not torch.isnan(planned).any()
+        graph_out = torch.empty_like(queries)
+        side = torch.cuda.Stream(device=device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side), torch.cuda.graph(graph, stream=side):
+            _hip.paged_decode_attention(graph_out, queries, pool, 9, tables, lens, partition_blocks=parts, work_items=items, separate_reduce=separate)
+        torch.cuda.current_stream(device).wait_stream(side)
+        for _ in range(3):
+            graph_out.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(graph_out, full), parts
+    rows = [0, 1, 2, 3, 40]
+    w.lengths = lengths
+    for b, (oracle, fp64) in _oracle_rows(pool, 9, w, queries, rows).items():
+        got = planned[b : b + 1].reshape(1, 32, 1, 64).cpu()
+        torch.testing.assert_close(got, oracle, **TOL)
+        torch.testing.assert_close(got, fp64, **TOL)
+
+
+def test_cached_scratch_survives_changing_shapes(device):
+    """Calls of different batch sizes, table widths and partition sizes share the cached
+    per-stream scratch; each must still match the oracle."""
+    pool = _random_pool(device, 1024, 17)
+    for batch, hi, parts, layer in ((3, 300, 4, 1), (9, 1000, 7, 2), (2, 2048, 1, 3), (9, 900, 32, 4)):
+        w = workloads.batched_decode(batch=batch, lo=20, hi=hi, num_blocks=1024, seed=batch + hi)
+        queries = torch.from_numpy(w.queries(layer)).to(device)
+        out = torch.full_like(queries, float("nan"))
+        _hip.paged_decode_attention(
+            out, queries, pool, layer, torch.from_numpy(w.tables).to(device), torch.from_numpy(w.lengths).to(device),
+            partition_blocks=parts,
+        )
+        torch.cuda.synchronize()
+        for b, (oracle, fp64) in _oracle_rows(pool, layer, w, queries, range(batch)).items():
+            torch.testing.assert_close(out[b : b + 1].reshape(1, 32, 1, 64).cpu(), oracle, **TOL)
 
 
 def test_constant_values_return_the_constant(device):

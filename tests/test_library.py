@@ -7,6 +7,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 
 from pagedcore_amd import _hip
@@ -32,10 +33,15 @@ def test_library_exports_every_declared_symbol():
 
 def test_workspace_size_formula():
     lib = _hip.load()
-    # 64 sequences x 32 heads x ceil(128/32) partitions x (64 outputs + max + sum)
-    assert lib.pc_attn_workspace_floats(64, 128, 32) == 64 * 32 * 4 * 66
-    assert lib.pc_attn_workspace_floats(1, 8, 4) == 32 * 2 * 66
-    assert lib.pc_attn_workspace_floats(1, 8, 6) == 0  # partition size must be a multiple of 4
+    # partials: 64 sequences x 32 heads x ceil(128/32) partitions x 64 floats, then the
+    # (max, sum) pairs; 256 B aligned regions
+    out = 64 * 32 * 4 * 64 * 4
+    ml = 64 * 32 * 4 * 2 * 4
+    assert lib.pc_attn_workspace_bytes(64, 128, 32) == out + ml
+    assert lib.pc_attn_workspace_bytes(1, 8, 4) == 32 * 2 * 64 * 4 + 512
+    assert lib.pc_attn_workspace_bytes(1, 8, 6) == lib.pc_attn_workspace_bytes(1, 8, 4)
+    assert lib.pc_attn_workspace_bytes(1, 8, 0) == 0  # partitions hold 1..64 blocks
+    assert lib.pc_attn_workspace_bytes(1, 8, 65) == 0
 
 
 @pytest.mark.parametrize(
@@ -60,23 +66,68 @@ def test_append_rejects_invalid_arguments_without_a_gpu(args, needle):
         ({"layer": 22}, b"layer"),
         ({"batch": -1}, b"batch"),
         ({"max_blocks": 0}, b"max_blocks"),
-        ({"parts": 6}, b"partition_blocks"),
-        ({"parts": 256}, b"partition_blocks"),
+        ({"parts": 0}, b"partition_blocks"),
+        ({"parts": 65}, b"partition_blocks"),
         ({"ws": None}, b"workspace"),
+        ({"ws": 272}, b"aligned"),
         ({"query": 8}, b"aligned"),
+        ({"out": 260}, b"aligned"),
+        ({"flags": 6}, b"flags"),
+        ({"tickets": None}, b"tickets"),
+        ({"tickets": 258}, b"aligned"),
+        ({"blocks": 2**31}, b"num_blocks"),
+        ({"items": 258}, b"aligned"),
+        ({"items": 256, "nitems": -1}, b"num_work_items"),
+        ({"items": 256, "nitems": 5}, b"num_work_items"),  # batch 1 x 4 partitions
     ],
 )
 def test_attention_rejects_invalid_arguments_without_a_gpu(overrides, needle):
     lib = _hip.load()
-    a = {"out": 16, "query": 16, "pool": 16, "blocks": 10, "layer": 0, "tables": 16, "max_blocks": 128,
-         "lens": 16, "batch": 1, "parts": 32, "ws": 16}
+    a = {"out": 256, "query": 256, "pool": 256, "blocks": 10, "layer": 0, "tables": 256, "max_blocks": 128,
+         "lens": 256, "batch": 1, "parts": 32, "items": None, "nitems": 0, "ws": 256, "tickets": 256, "flags": 0}
     a.update(overrides)
     status = lib.pc_paged_decode_attn(
         a["out"], a["query"], a["pool"], a["blocks"], a["layer"], a["tables"], a["max_blocks"], a["lens"],
-        a["batch"], a["parts"], a["ws"], a["ws"], None,
+        a["batch"], a["parts"], a["items"], a["nitems"], a["ws"], a["tickets"], a["flags"], None,
     )
     assert status == 1
     assert needle in lib.pc_last_error()
+
+
+def _plan_by_enumeration(lengths, max_blocks, partition_blocks):
+    rows = []
+    for b, length in enumerate(lengths):
+        if length <= 0:
+            continue
+        blocks = min(-(-int(length) // 16), max_blocks)
+        rows += [(b, p) for p in range(-(-blocks // partition_blocks))]
+    return rows
+
+
+@pytest.mark.parametrize("partition_blocks", [1, 3, 16, 64])
+def test_decode_plan_lists_every_partition_once(partition_blocks):
+    """pc_attn_plan (host code) against a direct enumeration, on ragged lengths including
+    zero-length rows, exact block multiples and lengths clamped by the table width."""
+    rng = np.random.default_rng(partition_blocks)
+    lengths = rng.integers(0, 2049, size=97).astype(np.int32)
+    lengths[:6] = [0, 1, 16, 17, 2048, 5000]  # 5000 tokens exceed the 128-block width: clamped
+    plan = _hip.plan_work_items(lengths, 128, partition_blocks)
+    assert plan.dtype == np.int32 and plan.shape[1] == 2
+    assert [tuple(r) for r in plan.tolist()] == _plan_by_enumeration(lengths, 128, partition_blocks)
+
+
+def test_decode_plan_rejects_bad_arguments():
+    lib = _hip.load()
+    lens = np.array([100, 200], dtype=np.int32)
+    items = np.zeros((2, 2), dtype=np.int32)
+    assert lib.pc_attn_plan(lens.ctypes.data, 2, 16, 4, items.ctypes.data, 2) == -1  # needs 1 + 4 pairs
+    assert b"capacity" in lib.pc_last_error()
+    assert lib.pc_attn_plan(lens.ctypes.data, 2, 16, 0, items.ctypes.data, 2) == -1
+    assert b"partition_blocks" in lib.pc_last_error()
+    assert lib.pc_attn_plan(None, 2, 16, 4, items.ctypes.data, 2) == -1
+    assert lib.pc_attn_plan_capacity(2, 16, 4) == 8
+    assert lib.pc_attn_plan_capacity(2, 16, 65) == -1
+    assert lib.pc_attn_plan(None, 0, 16, 4, None, 0) == 0  # empty batch: nothing to plan
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
