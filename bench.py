@@ -75,10 +75,10 @@ class DecodeLayers:
         self.max_blocks = int(w.tables.shape[1])
         nbytes = int(self.lib.pc_attn_workspace_bytes(w.batch, self.max_blocks, partition_blocks))
         self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
-        self.tickets = torch.zeros(w.batch * 4, dtype=torch.int32, device=device)
+        self.tickets = torch.zeros(w.batch, dtype=torch.int32, device=device)
         # One decode plan per step, shared by the 22 layers (built from the host lengths,
         # like the block tables).
-        self.items = torch.from_numpy(_hip.plan_work_items(w.lengths, self.max_blocks, partition_blocks)).to(device)
+        self.items = torch.from_numpy(_hip.plan_work_items(w.lengths, w.tables, partition_blocks)).to(device)
 
     def launch(self, layer: int, stream: int) -> None:
         status = self.lib.pc_paged_decode_attn(

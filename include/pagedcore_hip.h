@@ -72,29 +72,31 @@ int pc_kv_append(void* pool, int64_t num_blocks, int32_t layer_begin, int32_t nu
  *   out          [batch][32][64] fp16, contiguous, 16-byte aligned (query and pool too)
  *   block_tables [batch][max_blocks] int32 physical block ids (row b lists sequence b's
  *                blocks in logical order; only the first ceil(len/16) are read)
- *   context_lens [batch] int32, each in [1, max_blocks * 16]
+ *   context_lens [batch] int32, each in [1, max_blocks * 16] (0 or less: row not written)
  *   out[b][h] = softmax(q[b][h] . K[b][:len]^T / 8) . V[b][:len], computed in fp32 and
  *   rounded once to fp16. Slots past len are never multiplied, so poisoned (NaN) tail
  *   slots do not reach the output. A block id outside [0, num_blocks) is never
  *   dereferenced; its sequence's output rows become NaN.
  *
- * Long contexts are split into partitions of `partition_blocks` blocks (1..64), one wave
- * per (partition, kv head). By default the last wave to finish a (sequence, kv head)
- * merges that sequence's partitions (one launch); flags = PC_ATTN_SEPARATE_REDUCE merges
- * them in a second kernel instead.
- *   work_items  null: the grid covers batch * ceil(max_blocks / partition_blocks)
- *               partition slots and the slots past a sequence's length exit at once;
- *               otherwise the host-built plan from pc_attn_plan() for the same
- *               context_lens, block_tables width and partition_blocks (device int32
- *               pairs, num_work_items of them): the grid then holds only partitions
- *               that exist. A plan that does not match context_lens leaves rows unwritten.
- *               One plan serves every layer of a decode step.
+ * Split-K: a sequence's table is cut into work items of `partition_blocks` blocks (1, 2,
+ * 4 or 8), one workgroup per item and one wave per block. A sequence covered by one item
+ * is written directly; longer ones leave one partial per item in the workspace, merged
+ * by a second kernel (flags = PC_ATTN_SEPARATE_REDUCE) or, flags = 0, by the last
+ * workgroup of the sequence to finish (one launch).
+ *   work_items  null: the grid covers batch * ceil(max_blocks / partition_blocks) item
+ *               slots and the slots past a sequence's length exit at once; otherwise the
+ *               host-built plan from pc_attn_plan() for the same context_lens,
+ *               block_tables and partition_blocks (device copy, num_work_items records):
+ *               the grid then holds only items that exist, and the item kernel takes
+ *               block ids and lengths from the plan. A plan that does not match the
+ *               tables gives wrong rows (never an out-of-pool read). One plan serves
+ *               every layer of a decode step.
  *   workspace  fp32 partials, pc_attn_workspace_bytes() bytes, 256-byte aligned; scratch,
- *              nothing in it needs to survive between calls (unused when no sequence
- *              needs more than one partition);
- *   tickets    int32 [batch * 4], one merge ticket per (sequence, kv head), only read by
- *              the fused merge: ZERO-FILLED BEFORE ITS FIRST USE; every call leaves the
- *              tickets at zero again, so one ticket array serves any number of later calls.
+ *              nothing in it needs to survive between calls (unused, may be null, when
+ *              max_blocks <= partition_blocks);
+ *   tickets    int32 [batch], one merge ticket per sequence, only read by the fused merge:
+ *              ZERO-FILLED BEFORE ITS FIRST USE; every call leaves the tickets at zero
+ *              again, so one ticket array serves any number of later calls.
  * Calls that share a workspace or tickets must not overlap (use one set per stream).
  */
 #define PC_ATTN_SEPARATE_REDUCE 1
@@ -109,21 +111,29 @@ int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t
 int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t partition_blocks);
 
 /*
- * Host-side decode plan (no device access). context_lens and work_items are HOST
- * memory here. Writes one (sequence, partition) int32 pair per partition that exists,
- * sequence-major, and returns how many; returns -pc_status on invalid arguments or if
- * `capacity` (in pairs) is too small. pc_attn_plan_capacity() gives a capacity that
- * always suffices (-1 on invalid arguments).
+ * Host-side decode plan (no device access). context_lens [batch] and block_tables
+ * [batch][max_blocks] are HOST copies of the tables the attention call will receive;
+ * work_items is HOST memory. Writes one record of pc_attn_plan_record_ints() int32 per
+ * work item that exists -- items of partition_blocks blocks first (sequence-major), then
+ * the shorter tail items by descending block count, since workgroups are dispatched in
+ * record order:
+ *   {sequence, item, context length, 0, block ids of the item's partition_blocks blocks
+ *    (0 past the sequence's last block), 0 padding}
+ * and returns how many; returns -pc_status on invalid arguments or if `capacity` (in
+ * records) is too small. pc_attn_plan_capacity() gives a capacity that always suffices
+ * (-1 on invalid arguments). The kernel reads a record with one load, so the block
+ * loads of a work item wait for one round trip instead of two.
  *
  * Replaces nothing in the reference: PagedCore walks each sequence's pages in Python
  * (reference src/pagedcore/attention.py:31-53); the plan is what lets one launch cover a
- * ragged batch without idle waves.
+ * ragged batch without idle workgroups.
  */
-int32_t pc_attn_plan(const int32_t* context_lens, int32_t batch, int32_t max_blocks,
-                     int32_t partition_blocks, int32_t* work_items, int64_t capacity);
+int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, int32_t batch,
+                     int32_t max_blocks, int32_t partition_blocks, int32_t* work_items, int64_t capacity);
+int32_t pc_attn_plan_record_ints(int32_t partition_blocks);
 int64_t pc_attn_plan_capacity(int32_t batch, int32_t max_blocks, int32_t partition_blocks);
 
-/* Default partition size (blocks) used by the Python layer. */
+/* Default blocks per work item (partition_blocks) used by the Python layer. */
 int32_t pc_attn_default_partition_blocks(void);
 
 #ifdef __cplusplus

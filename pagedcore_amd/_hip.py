@@ -17,7 +17,7 @@ import numpy as np
 import torch
 from torch import Tensor
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 LIBRARY_NAME = "libpagedcore_hip.so"
 
 _lock = threading.Lock()
@@ -50,7 +50,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pc_paged_decode_attn.restype = ctypes.c_int
     lib.pc_paged_decode_attn.argtypes = [_p, _p, _p, _i64, _i32, _p, _i32, _p, _i32, _i32, _p, _i32, _p, _p, _i32, _p]
     lib.pc_attn_plan.restype = _i32
-    lib.pc_attn_plan.argtypes = [_p, _i32, _i32, _i32, _p, _i64]
+    lib.pc_attn_plan.argtypes = [_p, _p, _i32, _i32, _i32, _p, _i64]
+    lib.pc_attn_plan_record_ints.restype = _i32
+    lib.pc_attn_plan_record_ints.argtypes = [_i32]
     lib.pc_attn_plan_capacity.restype = _i64
     lib.pc_attn_plan_capacity.argtypes = [_i32, _i32, _i32]
 
@@ -154,15 +156,15 @@ def attention_workspace(device: torch.device, nbytes: int) -> Tensor:
 
 
 def merge_tickets(device: torch.device, batch: int) -> Tensor:
-    """Merge tickets (int32, one per sequence and kv head) for the current stream.
+    """Merge tickets (int32, one per sequence) for the current stream.
 
     Zero-filled when created or grown; the kernel leaves every ticket at zero after each
     call, so the array is reused as is.
     """
     key = _stream_key(device)
     tickets = _tickets.get(key)
-    if tickets is None or tickets.numel() < batch * 4:
-        tickets = torch.zeros(max(batch * 4, 64), dtype=torch.int32, device=device)
+    if tickets is None or tickets.numel() < batch:
+        tickets = torch.zeros(max(batch, 64), dtype=torch.int32, device=device)
         _tickets[key] = tickets
     return tickets
 
@@ -171,17 +173,24 @@ def workspace_bytes(batch: int, max_blocks: int, partition_blocks: int) -> int:
     return int(load().pc_attn_workspace_bytes(batch, max_blocks, partition_blocks))
 
 
-def plan_work_items(context_lens: np.ndarray, max_blocks: int, partition_blocks: int) -> np.ndarray:
-    """Host decode plan: int32 [items, 2] (sequence, partition) rows for every partition
-    that exists, computed by pc_attn_plan from host context lengths."""
+def plan_work_items(context_lens: np.ndarray, block_tables: np.ndarray, partition_blocks: int) -> np.ndarray:
+    """Host decode plan: int32 [items, record_ints] records {sequence, item, context
+    length, 0, the item's block ids} for every work item that exists, computed by
+    pc_attn_plan from HOST copies of the lengths and block tables [batch, max_blocks]."""
     lib = load()
     lens = np.ascontiguousarray(context_lens, dtype=np.int32)
+    tables = np.ascontiguousarray(block_tables, dtype=np.int32)
     batch = int(lens.shape[0])
+    if tables.ndim != 2 or tables.shape[0] != batch:
+        raise HipExtensionError("block_tables must be [batch, max_blocks] matching context_lens")
+    max_blocks = int(tables.shape[1])
+    fields = int(lib.pc_attn_plan_record_ints(partition_blocks))
     capacity = int(lib.pc_attn_plan_capacity(batch, max_blocks, partition_blocks))
-    if capacity < 0:
+    if fields < 0 or capacity < 0:
         _check(lib, "pc_attn_plan_capacity", 1)
-    items = np.empty((max(capacity, 1), 2), dtype=np.int32)
-    count = int(lib.pc_attn_plan(lens.ctypes.data, batch, max_blocks, partition_blocks, items.ctypes.data, capacity))
+    items = np.empty((max(capacity, 1), fields), dtype=np.int32)
+    count = int(lib.pc_attn_plan(lens.ctypes.data, tables.ctypes.data, batch, max_blocks, partition_blocks,
+                                 items.ctypes.data, capacity))
     if count < 0:
         _check(lib, "pc_attn_plan", -count)
     return items[:count]
@@ -204,11 +213,13 @@ def paged_decode_attention(
     """out[b] = paged decode attention of query[b] over layer `layer` of the pool.
 
     out/query: fp16 [batch, 32, 64] contiguous; block_tables: int32 [batch, max_blocks]
-    contiguous; context_lens: int32 [batch]. All on the pool's device. `work_items`: the
-    plan_work_items() rows for the same lengths, table width and partition size, as a
-    contiguous int32 device tensor (None: full grid). `workspace` (uint8) and `tickets`
-    (int32 [>= batch*4], zero-filled before first use) default to per-stream cached
-    buffers. `separate_reduce` None: DEFAULT_SEPARATE_REDUCE.
+    contiguous; context_lens: int32 [batch]. All on the pool's device. `partition_blocks`
+    (1, 2, 4 or 8; None: the library default) is the number of blocks one workgroup
+    covers, one wave per block. `work_items`: the plan_work_items() rows for the same
+    lengths, table width and partition size, as a contiguous int32 device tensor (None:
+    full grid). `workspace` (uint8) and `tickets` (int32 [>= batch], zero-filled before
+    first use) default to per-stream cached buffers. `separate_reduce` None:
+    DEFAULT_SEPARATE_REDUCE.
     """
     if separate_reduce is None:
         separate_reduce = DEFAULT_SEPARATE_REDUCE
@@ -224,13 +235,14 @@ def paged_decode_attention(
         raise HipExtensionError(f"workspace needs {nbytes} bytes")
     if tickets is None:
         tickets = merge_tickets(pool.device, batch)
-    elif tickets.dtype != torch.int32 or tickets.numel() < batch * 4:
-        raise HipExtensionError(f"tickets must be int32 with at least {batch * 4} entries")
+    elif tickets.dtype != torch.int32 or tickets.numel() < batch:
+        raise HipExtensionError(f"tickets must be int32 with at least {batch} entries")
     if work_items is not None and (
-        work_items.dtype != torch.int32 or work_items.dim() != 2 or work_items.shape[1] != 2
+        work_items.dtype != torch.int32 or work_items.dim() != 2
+        or work_items.shape[1] != int(lib.pc_attn_plan_record_ints(parts))
         or not work_items.is_contiguous()
     ):
-        raise HipExtensionError("work_items must be a contiguous int32 [items, 2] tensor")
+        raise HipExtensionError("work_items must be a contiguous int32 plan_work_items() array for this partition size")
     status = lib.pc_paged_decode_attn(
         out.data_ptr(),
         query.data_ptr(),

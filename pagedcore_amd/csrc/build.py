@@ -25,6 +25,10 @@ FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA results stay in VGPRs (no accumulator-register round trip before the VALU
+    # uses them).
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
 ]
 
 

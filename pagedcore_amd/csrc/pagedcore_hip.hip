@@ -20,7 +20,7 @@
 
 namespace {
 
-constexpr int kAbiVersion = 5;
+constexpr int kAbiVersion = 6;
 constexpr int kLayers = 22;
 constexpr int kSlots = 16;
 constexpr int kKVHeads = 4;
@@ -141,28 +141,31 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_word_kernel(
 // ---------------------------------------------------------------------------------------
 // Paged decode attention.
 //
-// One wave per (sequence b, kv head h, partition p); the partition's blocks are walked in
-// order with the next block's loads in flight. Nothing is shared between waves, so there
-// is no barrier and LDS holds only the p exchange (1.25 KiB per wave). Per 16-token block:
-//   * QK on the matrix core: S^T[16 tokens][16] = K[16][64] . Q^T[64][16] with two
-//     v_mfma_f32_16x16x32_f16 (q heads 8..15 are zero padding). K fragments come straight
-//     from HBM with 16 B loads, rows = tokens; fp16 x fp16 products are exact in fp32.
-//     Lane (c = lane % 16, g = lane / 16) receives the scores of q head c for tokens
-//     4g..4g+3.
-//   * online softmax in fp32 in the raw-dot domain (m = max q.k); p = 2^((dot - m) * C)
-//     with C = log2(e)/8, so the 1/8 scale is applied after the exact difference. The
-//     block max of each q head is taken over the 4 token groups with two permlane swaps,
-//     so all groups share one running max, and that max only moves when a block beats it
-//     by more than 2^8 (so rescales are rare and p <= 256).
-//   * p goes through LDS to the PV layout; PV is fp32 FMA on the VALU with fp16 V
-//     operands (v_fma_mix). Lane (c, g) owns dims 4c..4c+3 of all 8 q heads for tokens
-//     4g..4g+3 (8 B V loads; one load instruction covers 4 rows of 128 B).
-// At the end the 4 token groups are summed in registers by a permlane reduce-scatter, and
-// each lane holds one dim of every q head. A single-partition sequence writes fp16 output
-// directly. Otherwise the partial (m, l, o) goes to the workspace and the last wave of the
-// (sequence, head) to finish -- found with an atomic ticket -- merges all partitions, so
-// split-K needs no second launch (a separate reduce kernel is kept behind
-// PC_ATTN_SEPARATE_REDUCE).
+// Split-K over work items: item i of sequence b covers blocks [W i, W i + W) of its table
+// (W = partition_blocks, 1/2/4/8) for all 4 kv heads. One workgroup of W waves per item;
+// wave w owns block W i + w and issues every load of that block at once:
+//   * K, 8 KiB: per kv head h two 16 B loads per lane, lane (c = lane % 16, g = lane / 16)
+//     taking K[slot c][h][8g .. 8g + 7] and [32 + 8g ..] -- already the A operand of
+//     v_mfma_f32_16x16x32_f16;
+//   * V, 8 KiB: eight 16 B loads per lane, each instruction one contiguous KiB (whole 128 B
+//     lines), staged through LDS rows of 512 B + 32 B pad.
+// No wave ever waits for a second round of loads, so the whole grid's requests are in the
+// memory queues at once and the kernel drains HBM at its streaming rate.
+//
+// Per kv head (all in registers, one block so no online rescaling):
+//   * S^T[16 tokens][16] = K . Q^T on the matrix core (columns 8..15 repeat q heads 0..7);
+//     lane (c, g) receives the raw dots of q head 8h + c % 8 for tokens 4g .. 4g + 3;
+//   * masked tokens (past the context) become -inf and their V rows are zeroed in LDS,
+//     so poisoned tail slots never reach a product (0 x NaN would);
+//   * p = 2^((dot - max) log2(e) / 8): the 1/8 scale is applied to the exact difference;
+//   * O[16][16 dims] += P . V with v_mfma_f32_16x16x16f16: rows 0..7 carry the fp16
+//     rounding of p, rows 8..15 the remainder scaled by 2^18, so the product keeps fp32
+//     accuracy; V reaches the B layout through transposing LDS reads (ds_read_b64_tr_b16).
+// The W waves then meet in LDS: each thread folds D = 32 / W outputs of one q head over
+// the waves (max / rescale / sum). A sequence that fits one item writes fp16 output;
+// otherwise the item's (max, sum, unnormalized output) goes to the workspace and the
+// sequence's items are merged by paged_decode_merge_kernel, or -- flags 0 -- by the last
+// workgroup of the sequence to finish (atomic ticket).
 // ---------------------------------------------------------------------------------------
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -172,30 +175,25 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kAttnThreads = 64;   // one wave per (sequence, kv head, partition)
-constexpr int kMergeThreads = 64;  // separate merge kernel: one wave per (sequence, kv head)
-constexpr int kDefaultPartitionBlocks = 16;
-constexpr int kRing = 4;  // K/V blocks per wave whose loads are in flight together
-constexpr int kMaxPartitionBlocks = 64;  // one block id per lane
-constexpr int kVRowBytes = 136;  // LDS row of staged V: 64 fp16 dims + 8 B pad (spreads banks)
-constexpr int kMergeBatch = 8;   // partitions whose partials one merge round trip loads
+constexpr int kDefaultPartitionBlocks = 8;
+constexpr int kVPitch = 544;                   // bytes per staged V row: 512 B of data + 32 B pad
+constexpr int kWaveLds = kSlots * kVPitch;     // 8704 B of LDS per wave
+constexpr int kItemOutputs = kQHeads * kHeadDim;  // 2048 fp32 outputs per item
+constexpr int kMergeThreads = 256;             // separate merge: one workgroup per (sequence, 8 q heads)
+// Plan record: {sequence, item, context length, closer flag, block ids of the item's W
+// blocks (0 past the sequence's last block)}, padded to a multiple of 4 int32.
+constexpr int kPlanHeader = 4;
+// Ticket polls a closer makes before giving up on its siblings (each a round trip of about
+// a microsecond plus a short sleep): ends the wait well under a second in any case.
+constexpr int kCloserPolls = 1 << 16;
+constexpr int plan_fields(int w) { return kPlanHeader + (w + 3) / 4 * 4; }
 // log2(e) / sqrt(64): turns a raw q.k difference into a base-2 exponent.
 constexpr float kScoreToLog2 = 0.18033688011112042f;
-// Lazy-rescale threshold in raw-dot units (2^8 in probability terms).
-constexpr float kRescaleDot = 8.0f / kScoreToLog2;
 // Scale of the low (remainder) part of p in the PV product (2^18).
 constexpr float kLowScale = 262144.0f;
-
-struct BlockFrag {
-  half8_t k0, k1;  // K[token c][dims 8g..8g+7] and [32+8g..32+8g+7]
-  half4_t v[4];    // V[token 4g+j][dims 4c..4c+3]
-};
+static_assert(kWaveLds >= (kItemOutputs + 2 * kQHeads) * 4, "a wave's LDS also holds its partial");
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
-
-__device__ __forceinline__ float lane_value(float x, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
-}
 
 // Max / sum over the 4 lanes l, l^16, l^32, l^48 (one q head's 4 token groups); every
 // lane gets the result.
@@ -213,136 +211,20 @@ __device__ __forceinline__ float sum_over_groups(float x) {
   return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
-// Reduce-scatter over the wave halves: lanes < 32 get x[l] + x[l + 32], lanes >= 32 get
-// y[l - 32] + y[l].
-__device__ __forceinline__ float add_swap32(float x, float y) {
+// Reduce-scatter of a PV tile pair over the wave halves: lanes < 32 get
+// x[l] + x[l + 32] / 2^18, lanes >= 32 get y[l - 32] + y[l] / 2^18 (the high rows of a
+// 16x16 tile sit in lanes 0..31, its scaled low rows in lanes 32..63).
+__device__ __forceinline__ float fold_low_rows(float x, float y) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  return fmaf(__uint_as_float(r[1]), 1.0f / kLowScale, __uint_as_float(r[0]));
 }
 
-struct WaveState {
-  float m_run;      // running max of raw q.k, q head c % 8 (the same in every lane of that head)
-  float l_part;     // sum of p over this lane's 4 tokens of every block, q head c % 8
-  float4_t acc[4];  // PV tiles: acc[nt][r] = sum over tokens of A[row 4g + r] * V[dim 16nt + c],
-                    // rows 0..7 from the fp16 roundings of p, rows 8..15 from the scaled remainders
-};
-
-struct BlockSource {
-  const _Float16* kpool;  // K plane of the layer
-  const _Float16* vpool;  // V plane of the layer
-  uint32_t num_blocks;
-  int kofs, vofs;  // lane offsets inside a block
-};
-
-// Loads one block's K/V fragments. `ids` holds the partition's block ids, one per lane;
-// `i` is wave-uniform, so the id lands in an SGPR and the block base is scalar
-// arithmetic. Returns 1 if the block id is out of range (the fragments then come from
-// block 0 so that no access leaves the pool).
-__device__ __forceinline__ int load_block(BlockFrag& f, const BlockSource& src, int ids, int i) {
-  uint32_t phys = static_cast<uint32_t>(__builtin_amdgcn_readlane(ids, i));
-  int bad = 0;
-  if (phys >= src.num_blocks) {  // negative ids wrap to huge values
-    bad = 1;
-    phys = 0;
-  }
-  const _Float16* kblk = src.kpool + static_cast<int64_t>(phys) * kBlockElems;
-  const _Float16* vblk = src.vpool + static_cast<int64_t>(phys) * kBlockElems;
-  f.k0 = *reinterpret_cast<const half8_t*>(kblk + src.kofs);
-  f.k1 = *reinterpret_cast<const half8_t*>(kblk + src.kofs + 32);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    f.v[j] = *reinterpret_cast<const half4_t*>(vblk + src.vofs + j * kRowElems);
-  }
-  return bad;
-}
-
-// Value of head-indexed lane data for rows 4(g & 1) + r (r = 0..3) of this lane.
-__device__ __forceinline__ float row_head_value(float x, int r, int g) {
-  return (g & 1) ? lane_value(x, 4 + r) : lane_value(x, r);
-}
-
-// One block: S = K Q^T on MFMA (lanes c and c + 8 compute the same q head), online
-// softmax, then O += P V on MFMA with P split into its fp16 rounding (rows 0..7) and the
-// scaled remainder (rows 8..15), so that the product keeps fp32 accuracy and range. V
-// reaches the MFMA B layout through LDS: row-major stores, transposing reads.
-__device__ __forceinline__ void process_block(WaveState& st, const BlockFrag& f, half8_t qa,
-                                              half8_t qb, int valid, int c, int g,
-                                              char* __restrict__ vlds) {
-  float4_t s = {0.f, 0.f, 0.f, 0.f};
-  s = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.k0, qa, s, 0, 0, 0);
-  s = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.k1, qb, s, 0, 0, 0);
-  // s[r] = q[head c % 8] . k[token 4g + r]
-  float sc[4] = {s[0], s[1], s[2], s[3]};
-  half4_t v[4] = {f.v[0], f.v[1], f.v[2], f.v[3]};
-  if (valid < kSlots) {  // last, partial block: masked slots never enter a product
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if (4 * g + r >= valid) {
-        sc[r] = -INFINITY;
-        v[r] = half4_t{};
-      }
-    }
-  }
-  // V rows to LDS early: the stores overlap the softmax arithmetic.
-#pragma unroll
-  for (int j = 0; j < 4; ++j) *reinterpret_cast<half4_t*>(vlds + (4 * g + j) * kVRowBytes + 8 * c) = v[j];
-
-  // Block max over all 16 tokens (finite: every block has a valid token).
-  const float mblk = max_over_groups(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-  if (__any(mblk > st.m_run + kRescaleDot)) {
-    const float m_new = fmaxf(st.m_run, mblk);
-    const float alpha = exp2_fast((st.m_run - m_new) * kScoreToLog2);  // 0 when m_run = -inf
-    st.l_part *= alpha;
-    st.m_run = m_new;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float a = row_head_value(alpha, r, g);
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) st.acc[nt][r] *= a;
-    }
-  }
-  float p[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    p[r] = (sc[r] == -INFINITY) ? 0.f : exp2_fast((sc[r] - st.m_run) * kScoreToLog2);
-  }
-  st.l_part += (p[0] + p[1]) + (p[2] + p[3]);
-  // A operand: row c holds p of head c % 8 for tokens 4g..4g+3: for c < 8 the fp16
-  // rounding of p, for c >= 8 the remainder scaled by 2^18. p <= 2^8 (lazy rescale)
-  // bounds the scaled remainder by 2^15, and the scale keeps p down to 2^-32 in fp16's
-  // normal range, so tiny probabilities still reach the value products.
-  half4_t hi, pa;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) hi[r] = static_cast<_Float16>(p[r]);
-  pa = hi;
-  if (c >= kGroup) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) pa[r] = static_cast<_Float16>((p[r] - static_cast<float>(hi[r])) * kLowScale);
-  }
-
+// LDS ordering inside one wave: the compiler keeps LDS accesses on their side of this
+// point and the wave's LDS operations complete in issue order.
+__device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // Lane (c, g) reads row 4g + c/4, dims 16nt + 4(c%4)..+3; the transposing read hands
-  // it V[tokens 4g..4g+3][dim 16nt + c], the B operand of the 16x16x16 MFMA.
-  const char* vrow = vlds + (4 * g + (c >> 2)) * kVRowBytes + 8 * (c & 3);
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const short4_t raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        reinterpret_cast<__attribute__((address_space(3))) short4_t*>(
-            reinterpret_cast<uintptr_t>(vrow + 32 * nt)));
-    st.acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, raw), st.acc[nt], 0, 0, 0);
-  }
-  // The next block rewrites vlds; LDS ops of one wave complete in order, and this fence
-  // keeps the compiler from hoisting those stores above these reads.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-}
-
-// Partition count of a sequence.
-__device__ __forceinline__ int partitions_of(int len, int max_blocks, int partition_blocks, int& nblk) {
-  nblk = min((len + kSlots - 1) / kSlots, max_blocks);
-  return (nblk + partition_blocks - 1) / partition_blocks;
 }
 
 struct AttnArgs {
@@ -352,28 +234,25 @@ struct AttnArgs {
   int64_t num_blocks;
   const int32_t* block_tables;
   const int32_t* context_lens;
-  float* ws_out;     // [batch*4][max_parts][8 q heads][64] unnormalized partial outputs
-  float* ws_ml;      // [batch*4][max_parts][8 q heads][2] (running max, sum of p)
-  int32_t* tickets;  // [batch*4] merge tickets, zero between calls
-  const int32_t* work_items;  // (sequence, partition) pairs, or null: every (sequence, partition slot)
-  int layer, max_blocks, batch, partition_blocks, max_parts, fused_merge;
+  float* ws_out;     // [batch][max_items][32 q heads][64] unnormalized item outputs
+  float* ws_ml;      // [batch][max_items][32 q heads][2] (max of raw dots, sum of p)
+  int32_t* tickets;  // [batch] merge tickets, zero between calls
+  const int32_t* work_items;  // (sequence, item) pairs, or null: every (sequence, item slot)
+  int layer, max_blocks, batch, max_items, fused_merge;
 };
 
-// Agent-coherent accesses (global_store / global_load ... sc1): they bypass this XCD's L2,
-// so partials published by one wave are visible to a wave on any XCD without a cache
-// writeback or invalidate. The plain variants serve the separate merge kernel, which
-// runs after the partition kernel has completed.
-template <bool kCoherent>
-__device__ __forceinline__ void store_partial(float* p, float x) {
-  if constexpr (kCoherent) {
-    __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
-    *p = x;
-  }
+// Items of a sequence (0 for an empty one); nblk = its block count, clamped to the table.
+__device__ __forceinline__ int items_of(int len, int max_blocks, int w, int& nblk) {
+  nblk = len > 0 ? min((len - 1) / kSlots + 1, max_blocks) : 0;
+  return (nblk + w - 1) / w;
 }
 
+// Agent-coherent accesses (global_store / global_load ... sc1): partials published by a
+// workgroup on one XCD are visible to a workgroup on any XCD without a cache writeback or
+// invalidate. The plain variants serve the separate merge kernel, which runs after the
+// item kernel has completed.
 template <bool kCoherent>
-__device__ __forceinline__ void store_partial2(float* p, float x, float y) {
+__device__ __forceinline__ void store_f2(float* p, float x, float y) {
   if constexpr (kCoherent) {
     const uint64_t bits = (static_cast<uint64_t>(__float_as_uint(y)) << 32) | __float_as_uint(x);
     __hip_atomic_store(reinterpret_cast<uint64_t*>(p), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -383,7 +262,7 @@ __device__ __forceinline__ void store_partial2(float* p, float x, float y) {
 }
 
 template <bool kCoherent>
-__device__ __forceinline__ float2_t load_partial2(const float* p) {
+__device__ __forceinline__ float2_t load_f2(const float* p) {
   if constexpr (kCoherent) {
     const uint64_t x = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
@@ -393,226 +272,388 @@ __device__ __forceinline__ float2_t load_partial2(const float* p) {
   }
 }
 
-template <bool kCoherent>
-__device__ __forceinline__ float4_t load_partial4(const float* p) {
-  if constexpr (kCoherent) {
-    const float2_t lo = load_partial2<true>(p);
-    const float2_t hi = load_partial2<true>(p + 2);
-    return float4_t{lo[0], lo[1], hi[0], hi[1]};
-  } else {
-    return *reinterpret_cast<const float4_t*>(p);
-  }
-}
+// Items whose partials one merge round trip loads, for D outputs per thread.
+constexpr int merge_batch(int d) { return d <= 2 ? 32 : (d <= 4 ? 16 : (d <= 8 ? 8 : 4)); }
 
-// Merges the nparts partials of one (sequence, kv head) and writes its 8 output rows.
-// Lane (qh = lane / 8, dl = lane % 8) folds every partition's dims 8dl..8dl+7 of q head
-// qh with the online softmax rule; the loads of kMergeBatch partitions are issued
-// before any of them is used, so a merge of up to kMergeBatch partitions costs one
-// round trip.
-template <bool kCoherent>
-__device__ __forceinline__ void merge_partitions(const AttnArgs& a, int bh, int nparts, int lane) {
-  const int qh = lane >> 3;
-  const int dl = lane & 7;
-  float m = -INFINITY, l = 0.f, o[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = 0.f;
-  const int64_t first = static_cast<int64_t>(bh) * a.max_parts;
+// Folds items [i_begin, nitems) of sequence b into the running state (m, l, o) for dims
+// [o0, o0 + D) of q head `qhead` (D even) with the online-softmax rule; the loads of
+// merge_batch(D) items are issued before any of them is used. Returns the normalized
+// outputs in `res`.
+template <bool kCoherent, int D>
+__device__ __forceinline__ void merge_items_from(const AttnArgs& a, int b, int i_begin, int nitems, int qhead, int o0,
+                                                 float m, float l, float (&o)[D], float (&res)[D]) {
+  constexpr int kBatch = merge_batch(D);
+  const int64_t first = static_cast<int64_t>(b) * a.max_items;
 #pragma unroll 1
-  for (int p0 = 0; p0 < nparts; p0 += kMergeBatch) {
-    float2_t ml[kMergeBatch];
-    float4_t x0[kMergeBatch], x1[kMergeBatch];
+  for (int i0 = i_begin; i0 < nitems; i0 += kBatch) {
+    float2_t ml[kBatch];
+    float2_t x[kBatch][D / 2];
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
-      const int64_t p = first + min(p0 + j, nparts - 1);  // clamped: always in bounds
-      ml[j] = load_partial2<kCoherent>(a.ws_ml + (p * kGroup + qh) * 2);
-      const float* xp = a.ws_out + (p * kGroup + qh) * kHeadDim + 8 * dl;
-      x0[j] = load_partial4<kCoherent>(xp);
-      x1[j] = load_partial4<kCoherent>(xp + 4);
+    for (int j = 0; j < kBatch; ++j) {
+      const int64_t p = first + min(i0 + j, nitems - 1);  // clamped: always in bounds
+      ml[j] = load_f2<kCoherent>(a.ws_ml + (p * kQHeads + qhead) * 2);
+      const float* xp = a.ws_out + p * kItemOutputs + qhead * kHeadDim + o0;
+#pragma unroll
+      for (int i = 0; i < D / 2; ++i) x[j][i] = load_f2<kCoherent>(xp + 2 * i);
     }
     // Branch-free fold (a branch would let the compiler sink each load to its use): a
-    // clamped duplicate gets weight 0; m is finite from partition 0 on, so m_new is too.
+    // clamped duplicate gets weight 0; m is finite from the first item on, so m_new is too.
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
-      const float mp = (p0 + j < nparts) ? ml[j][0] : -INFINITY;
+    for (int j = 0; j < kBatch; ++j) {
+      const float mp = (i0 + j < nitems) ? ml[j][0] : -INFINITY;
       const float m_new = fmaxf(m, mp);
       const float s_old = exp2_fast((m - m_new) * kScoreToLog2);  // 0 while m = -inf
       const float s_new = exp2_fast((mp - m_new) * kScoreToLog2);  // 0 for a duplicate
-      l = l * s_old + ml[j][1] * s_new;
+      // Explicit fmaf: every instantiation (and so both merge modes) rounds identically.
+      l = fmaf(ml[j][1], s_new, l * s_old);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        o[i] = o[i] * s_old + x0[j][i] * s_new;
-        o[4 + i] = o[4 + i] * s_old + x1[j][i] * s_new;
+      for (int i = 0; i < D / 2; ++i) {
+        o[2 * i] = fmaf(x[j][i][0], s_new, o[2 * i] * s_old);
+        o[2 * i + 1] = fmaf(x[j][i][1], s_new, o[2 * i + 1] * s_old);
       }
       m = m_new;
     }
   }
-  half8_t r;
+  const float inv = 1.0f / l;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = static_cast<_Float16>(o[i] / l);
-  *reinterpret_cast<half8_t*>(a.out + (static_cast<int64_t>(bh) * kGroup + qh) * kHeadDim + 8 * dl) = r;
+  for (int i = 0; i < D; ++i) res[i] = o[i] * inv;
 }
 
-__global__ __launch_bounds__(kAttnThreads) void paged_decode_partition_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) char lds_v[kSlots * kVRowBytes];  // V rows of one block
+template <bool kCoherent, int D>
+__device__ __forceinline__ void merge_items(const AttnArgs& a, int b, int nitems, int qhead, int o0, float (&res)[D]) {
+  float o[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) o[i] = 0.f;
+  merge_items_from<kCoherent, D>(a, b, 0, nitems, qhead, o0, -INFINITY, 0.f, o, res);
+}
 
-  const int h = blockIdx.x % kKVHeads;
-  const int rest = blockIdx.x / kKVHeads;
-  int b, part;
-  if (a.work_items) {  // planned grid: one item per existing partition
-    b = a.work_items[2 * rest];
-    part = a.work_items[2 * rest + 1];
-    if (static_cast<uint32_t>(b) >= static_cast<uint32_t>(a.batch) || part < 0) return;
-  } else {  // full grid: partition slots past a sequence's length exit below
-    b = rest % a.batch;
-    part = rest / a.batch;
+// The closer's fold: items [0, nitems) of sequence b in item order with the same
+// arithmetic as merge_items, item `own` taken from registers (m_own, l_own, x_own) and the
+// others through agent-coherent loads. Unused batch slots and the own item's (never
+// written) workspace entries are selected out, never multiplied, so the result is
+// bit-identical to the separate merge.
+template <int D>
+__device__ __forceinline__ void merge_with_own(const AttnArgs& a, int b, int nitems, int own, int qhead, int o0,
+                                               float m_own, float l_own, const float (&x_own)[D], float (&res)[D]) {
+  constexpr int kBatch = merge_batch(D);
+  float m = -INFINITY, l = 0.f, o[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) o[i] = 0.f;
+  const int64_t first = static_cast<int64_t>(b) * a.max_items;
+#pragma unroll 1
+  for (int i0 = 0; i0 < nitems; i0 += kBatch) {
+    float2_t ml[kBatch];
+    float2_t x[kBatch][D / 2];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int64_t p = first + min(i0 + j, nitems - 1);  // clamped: always in bounds
+      ml[j] = load_f2<true>(a.ws_ml + (p * kQHeads + qhead) * 2);
+      const float* xp = a.ws_out + p * kItemOutputs + qhead * kHeadDim + o0;
+#pragma unroll
+      for (int i = 0; i < D / 2; ++i) x[j][i] = load_f2<true>(xp + 2 * i);
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int idx = i0 + j;
+      const bool used = idx < nitems;
+      const bool mine = idx == own;
+      const float mp = !used ? -INFINITY : (mine ? m_own : ml[j][0]);
+      const float lp = !used ? 0.f : (mine ? l_own : ml[j][1]);
+      const float m_new = fmaxf(m, mp);
+      const float s_old = exp2_fast((m - m_new) * kScoreToLog2);
+      const float s_new = exp2_fast((mp - m_new) * kScoreToLog2);
+      l = fmaf(lp, s_new, l * s_old);
+#pragma unroll
+      for (int i = 0; i < D / 2; ++i) {
+        const float x0 = !used ? 0.f : (mine ? x_own[2 * i] : x[j][i][0]);
+        const float x1 = !used ? 0.f : (mine ? x_own[2 * i + 1] : x[j][i][1]);
+        o[2 * i] = fmaf(x0, s_new, o[2 * i] * s_old);
+        o[2 * i + 1] = fmaf(x1, s_new, o[2 * i + 1] * s_old);
+      }
+      m = m_new;
+    }
   }
-  const int lane = threadIdx.x;
+  const float inv = 1.0f / l;
+#pragma unroll
+  for (int i = 0; i < D; ++i) res[i] = o[i] * inv;
+}
+
+template <int D>
+__device__ __forceinline__ void store_out(_Float16* dst, const float (&v)[D]) {
+#pragma unroll
+  for (int i = 0; i < D; i += 2) {
+    *reinterpret_cast<half2_t*>(dst + i) = half2_t{static_cast<_Float16>(v[i]), static_cast<_Float16>(v[i + 1])};
+  }
+}
+
+template <int W>
+__global__ __launch_bounds__(64 * W) void paged_decode_item_kernel(AttnArgs a) {
+  constexpr int D = kItemOutputs / (64 * W);  // outputs per thread in the workgroup merge
+  __shared__ __attribute__((aligned(16))) char lds[W * kWaveLds];
+  __shared__ int32_t ticket_slot;
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int c = lane & 15;
   const int g = lane >> 4;
 
-  // One round trip: the length, this partition's block ids and Q are requested together.
-  const int pbeg = part * a.partition_blocks;
-  const int32_t* table = a.block_tables + static_cast<int64_t>(b) * a.max_blocks;
-  const int id_index = pbeg + lane;
-  const int ids = (lane < a.partition_blocks && id_index < a.max_blocks) ? table[id_index] : 0;
-  // MFMA B operand = Q^T: column c is q head h*8 + c % 8 (columns 8..15 repeat 0..7).
-  const _Float16* qrow = a.query + (static_cast<int64_t>(b) * kQHeads + h * kGroup + (c & 7)) * kHeadDim;
-  const half8_t qa = *reinterpret_cast<const half8_t*>(qrow + 8 * g);
-  const half8_t qb = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
-  const int len = a.context_lens[b];
-  if (len <= 0) return;
-  int nblk;
-  const int nparts = partitions_of(len, a.max_blocks, a.partition_blocks, nblk);
-  if (part >= nparts) return;
-  const int count = min(nblk - pbeg, a.partition_blocks);
-
-  BlockSource src;
-  const int64_t kind_elems = a.num_blocks * kBlockElems;
-  src.kpool = a.pool + static_cast<int64_t>(a.layer) * 2 * kind_elems;
-  src.vpool = src.kpool + kind_elems;
-  src.num_blocks = static_cast<uint32_t>(a.num_blocks);  // host checks num_blocks < 2^31
-  src.kofs = c * kRowElems + h * kHeadDim + 8 * g;
-  src.vofs = 4 * g * kRowElems + h * kHeadDim + 4 * c;
-
-  WaveState st;
-  st.m_run = -INFINITY;
-  st.l_part = 0.f;
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt) st.acc[nt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  int bad = 0;
-
-  // Ring of kRing fragment buffers: while one block is processed, the loads of the next
-  // kRing - 1 blocks are in flight. Loads are unconditional (indices past the last block
-  // re-read it: in bounds, served by L2) so each block waits only for its own loads.
-  {
-    BlockFrag f[kRing];
-#pragma unroll
-    for (int j = 0; j < kRing; ++j) {
-      bad |= load_block(f[j], src, ids, min(j, count - 1));
-      __builtin_amdgcn_sched_barrier(0);  // issue order = use order
+  int b, item, len;
+  int32_t id;
+  bool closer;  // merges the sequence's items (fused merge)
+  const int blk_in_item = wave;
+  if (a.work_items) {
+    // Planned grid: one workgroup per item that exists. Its plan record (one uniform
+    // load) carries the sequence, the item, the context length and the item's block ids,
+    // so the KV loads leave after a single round trip.
+    const int32_t* rec = a.work_items + static_cast<int64_t>(blockIdx.x) * plan_fields(W);
+    b = rec[0];
+    item = rec[1];
+    len = rec[2];
+    closer = rec[3] != 0;
+    id = rec[kPlanHeader + blk_in_item];
+    if (static_cast<uint32_t>(b) >= static_cast<uint32_t>(a.batch) ||
+        static_cast<uint32_t>(item) >= static_cast<uint32_t>(a.max_items)) {
+      return;
     }
-    for (int i = 0; i < count; i += kRing) {
+  } else {
+    // Full grid: item slots past a sequence's length exit below; the length and this
+    // wave's block id come from the device tables in one round trip.
+    b = blockIdx.x % a.batch;
+    item = blockIdx.x / a.batch;
+    id = a.block_tables[static_cast<int64_t>(b) * a.max_blocks + min(item * W + blk_in_item, a.max_blocks - 1)];
+    len = a.context_lens[b];
+  }
+  const int blk = item * W + blk_in_item;
+  // B operand = Q^T per kv head h: column c is q head 8h + c % 8.
+  const _Float16* qrow = a.query + (static_cast<int64_t>(b) * kQHeads + (c & 7)) * kHeadDim + 8 * g;
+  half8_t qa[kKVHeads], qb[kKVHeads];
 #pragma unroll
-      for (int j = 0; j < kRing; ++j) {
-        __builtin_amdgcn_sched_barrier(0);  // keep the refills ahead of the next block's waits
-        if (i + j < count) process_block(st, f[j], qa, qb, len - (pbeg + i + j) * kSlots, c, g, lds_v);
-        bad |= load_block(f[j], src, ids, min(i + j + kRing, count - 1));
+  for (int h = 0; h < kKVHeads; ++h) {
+    qa[h] = *reinterpret_cast<const half8_t*>(qrow + h * kGroup * kHeadDim);
+    qb[h] = *reinterpret_cast<const half8_t*>(qrow + h * kGroup * kHeadDim + 32);
+  }
+  int nblk;
+  const int nitems = items_of(len, a.max_blocks, W, nblk);
+  if (item >= nitems) return;  // uniform over the workgroup
+  if (!a.work_items) closer = item == nitems - 1;  // the sequence's highest workgroup index
+  const bool active = blk < nblk;  // uniform over the wave; wave 0 is always active
+
+  char* vl = lds + wave * kWaveLds;
+  float* part = reinterpret_cast<float*>(vl);  // after PV: [32 q heads][64] outputs, then (m, l) pairs
+  if (active) {
+    uint32_t phys = static_cast<uint32_t>(id);
+    const bool bad = phys >= static_cast<uint64_t>(a.num_blocks);  // negative ids wrap to huge values
+    if (bad) phys = 0;  // never dereferenced out of the pool
+    const int64_t kind_elems = a.num_blocks * kBlockElems;
+    const _Float16* kblk = a.pool + static_cast<int64_t>(a.layer) * 2 * kind_elems + static_cast<int64_t>(phys) * kBlockElems;
+    const char* vblk = reinterpret_cast<const char*>(kblk + kind_elems);
+    half8_t k0[kKVHeads], k1[kKVHeads];
+#pragma unroll
+    for (int h = 0; h < kKVHeads; ++h) {
+      k0[h] = *reinterpret_cast<const half8_t*>(kblk + c * kRowElems + h * kHeadDim + 8 * g);
+      k1[h] = *reinterpret_cast<const half8_t*>(kblk + c * kRowElems + h * kHeadDim + 32 + 8 * g);
+    }
+    uint4 vraw[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) vraw[q] = *reinterpret_cast<const uint4*>(vblk + q * 1024 + lane * 16);
+
+    const int valid = len - blk * kSlots;  // >= 1; below 16 only in the sequence's last block
+    // V rows to LDS; in the sequence's last block the rows of masked slots are zeroed.
+    char* vdst = vl + (lane >> 5) * kVPitch + (lane & 31) * 16;
+    if (valid >= kSlots) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) *reinterpret_cast<uint4*>(vdst + 2 * q * kVPitch) = vraw[q];
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int slot = 2 * q + (lane >> 5);
+        *reinterpret_cast<uint4*>(vdst + 2 * q * kVPitch) = slot < valid ? vraw[q] : uint4{0, 0, 0, 0};
+      }
+    }
+    wave_lds_fence();
+
+    float o[kKVHeads][2][4];
+    float mh[kKVHeads], lh[kKVHeads];
+#pragma unroll
+    for (int h = 0; h < kKVHeads; ++h) {
+      float4_t s = {0.f, 0.f, 0.f, 0.f};
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0[h], qa[h], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1[h], qb[h], s, 0, 0, 0);
+      float sc[4] = {s[0], s[1], s[2], s[3]};
+      if (valid < kSlots) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] = 4 * g + r < valid ? sc[r] : -INFINITY;
+      }
+      // Block max of q head c % 8 over all 16 tokens (finite: token 0 is always valid).
+      const float mblk = max_over_groups(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+      float p[4];
+      // exp2(-inf) = 0: masked tokens get no weight.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = exp2_fast((sc[r] - mblk) * kScoreToLog2);
+      lh[h] = sum_over_groups((p[0] + p[1]) + (p[2] + p[3]));
+      mh[h] = mblk;
+      // A operand: row c holds p of q head c % 8 for tokens 4g .. 4g + 3: for c < 8 the
+      // fp16 rounding of p, for c >= 8 the remainder scaled by 2^18 (p <= 1 bounds it by
+      // 2^7, and the scale keeps p down to 2^-32 in fp16's normal range).
+      half4_t pa;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float hi = static_cast<float>(static_cast<_Float16>(p[r]));
+        pa[r] = static_cast<_Float16>(c >= kGroup ? (p[r] - hi) * kLowScale : p[r]);
+      }
+      // Lane (c, g) reads row 4g + c/4, dims 16nt + 4(c%4) .. + 3 of head h; the
+      // transposing read hands it V[tokens 4g .. 4g + 3][dim 16nt + c], the B operand.
+      const char* vrow = vl + (4 * g + (c >> 2)) * kVPitch + h * kHeadDim * 2 + 8 * (c & 3);
+      float4_t acc[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const short4_t raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            reinterpret_cast<__attribute__((address_space(3))) short4_t*>(reinterpret_cast<uintptr_t>(vrow + 32 * nt)));
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, raw),
+                                                        float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      }
+      // High rows plus unscaled low rows: lane (c, g) then holds q head 8h + 4(g & 1) + r,
+      // dim 16(2k + g / 2) + c (lanes g < 2 from tile 2k, g >= 2 from tile 2k + 1).
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[h][k][r] = fold_low_rows(acc[2 * k][r], acc[2 * k + 1][r]);
+    }
+    // The partial overwrites this wave's V rows: every PV read above has been issued.
+    wave_lds_fence();
+#pragma unroll
+    for (int h = 0; h < kKVHeads; ++h)
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qh = kGroup * h + 4 * (g & 1) + r;
+          part[qh * kHeadDim + 16 * (2 * k + (g >> 1)) + c] = bad ? NAN : o[h][k][r];
+        }
+    if (lane < kGroup) {
+#pragma unroll
+      for (int h = 0; h < kKVHeads; ++h) {
+        *reinterpret_cast<float2_t*>(part + kItemOutputs + (kGroup * h + lane) * 2) = float2_t{mh[h], lh[h]};
       }
     }
   }
+  __syncthreads();
 
-  // Add the high rows and the unscaled low rows: afterwards lane (c, g) holds o[k][r] =
-  // output of q head 4(g & 1) + r, dim 16(2k + g / 2) + c (lanes g < 2 from tile 2k,
-  // g >= 2 from 2k + 1).
-  const float l_sum = sum_over_groups(st.l_part);  // lane c < 8: q head c
-  const float row_scale = g >= 2 ? 1.0f / kLowScale : 1.0f;
-  float o[2][4];
+  // Workgroup merge: thread t folds outputs [t D, t D + D) -- q head t D / 64 -- over the
+  // item's active waves.
+  const int t = threadIdx.x;
+  const int qhead = (t * D) / kHeadDim;
+  const int o0 = (t * D) % kHeadDim;
+  const int nact = min(W, nblk - item * W);
+  float m = -INFINITY;
+  for (int w = 0; w < nact; ++w) {
+    m = fmaxf(m, reinterpret_cast<const float*>(lds + w * kWaveLds)[kItemOutputs + qhead * 2]);
+  }
+  float l = 0.f, acc[D];
 #pragma unroll
-  for (int k = 0; k < 2; ++k)
+  for (int i = 0; i < D; ++i) acc[i] = 0.f;
+  for (int w = 0; w < nact; ++w) {
+    const float* pw = reinterpret_cast<const float*>(lds + w * kWaveLds);
+    const float2_t ml = *reinterpret_cast<const float2_t*>(pw + kItemOutputs + qhead * 2);
+    const float e = exp2_fast((ml[0] - m) * kScoreToLog2);
+    l += ml[1] * e;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      o[k][r] = add_swap32(st.acc[2 * k][r] * row_scale, st.acc[2 * k + 1][r] * row_scale);
+    for (int i = 0; i < D; i += 4) {
+      const float4_t x = *reinterpret_cast<const float4_t*>(pw + qhead * kHeadDim + o0 + i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i + j] += x[j] * e;
     }
-  const int bh = b * kKVHeads + h;
-  const int64_t row0 = static_cast<int64_t>(bh) * kGroup;  // output row of q head 0
-  const int head0 = 4 * (g & 1);
-  const int dim0 = 16 * (g >> 1) + c;  // + 32k
-
-  if (nparts == 1) {
+  }
+  _Float16* out = a.out + (static_cast<int64_t>(b) * kQHeads + qhead) * kHeadDim + o0;
+  if (nitems == 1) {
+    float res[D];
+    const float inv = 1.0f / l;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float inv = 1.0f / row_head_value(l_sum, r, g);
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const float x = bad ? NAN : o[k][r] * inv;
-        a.out[(row0 + head0 + r) * kHeadDim + dim0 + 32 * k] = static_cast<_Float16>(x);
-      }
-    }
+    for (int i = 0; i < D; ++i) res[i] = acc[i] * inv;
+    store_out<D>(out, res);
     return;
   }
-  const int64_t pidx = static_cast<int64_t>(bh) * a.max_parts + part;
-  float* ws_out = a.ws_out + pidx * kGroup * kHeadDim;
-  float* ws_ml = a.ws_ml + pidx * kGroup * 2;
+  const int64_t pidx = static_cast<int64_t>(b) * a.max_items + item;
+  float* ws_out = a.ws_out + pidx * kItemOutputs + qhead * kHeadDim + o0;
+  float* ws_ml = a.ws_ml + (pidx * kQHeads + qhead) * 2;
   if (!a.fused_merge) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        store_partial<false>(ws_out + (head0 + r) * kHeadDim + dim0 + 32 * k, bad ? NAN : o[k][r]);
-      }
-    if (lane < kGroup) store_partial2<false>(ws_ml + lane * 2, st.m_run, l_sum);
+    for (int i = 0; i < D; i += 4) *reinterpret_cast<float4_t*>(ws_out + i) = float4_t{acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+    if (o0 == 0) store_f2<false>(ws_ml, m, l);
     return;
   }
 
-  // Last-arriver merge: publish the partial with agent-coherent stores, wait until they
-  // have completed, then take a ticket; the wave that draws nparts - 1 sees every other
-  // partial through agent-coherent loads, writes the output and re-arms the ticket.
+  // Fused merge. Every item but the closer publishes its partial with agent-coherent
+  // stores, waits until they have completed, then bumps the sequence's ticket. The closer
+  // (dispatched after all of them) waits -- a bounded number of polls -- until the ticket
+  // shows every sibling, folds the siblings' partials (agent-coherent loads) and its own
+  // (registers) in item order, writes the output and re-arms the ticket.
+  if (!closer) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      store_partial<true>(ws_out + (head0 + r) * kHeadDim + dim0 + 32 * k, bad ? NAN : o[k][r]);
-    }
-  if (lane < kGroup) store_partial2<true>(ws_ml + lane * 2, st.m_run, l_sum);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): every store of this wave has completed
-  int ticket = 0;
-  if (lane == 0) {
-    ticket = __hip_atomic_fetch_add(&a.tickets[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; i < D; i += 2) store_f2<true>(ws_out + i, acc[i], acc[i + 1]);
+    if (o0 == 0) store_f2<true>(ws_ml, m, l);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): every store of this thread has completed
+    __syncthreads();
+    if (t == 0) __hip_atomic_fetch_add(&a.tickets[b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
   }
-  ticket = __builtin_amdgcn_readfirstlane(ticket);
-  if (ticket != nparts - 1) return;
-  merge_partitions<true>(a, bh, nparts, lane);
-  if (lane == 0) __hip_atomic_store(&a.tickets[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (t == 0) {
+    int seen = 0;
+    for (int poll = 0; poll < kCloserPolls; ++poll) {
+      seen = __hip_atomic_load(&a.tickets[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (seen >= nitems - 1) break;
+      __builtin_amdgcn_s_sleep(8);
+    }
+    ticket_slot = seen;
+  }
+  __syncthreads();
+  float res[D];
+  if (ticket_slot != nitems - 1) {
+    // The siblings never all arrived within the poll budget: the row becomes NaN rather
+    // than a wait without end.
+#pragma unroll
+    for (int i = 0; i < D; ++i) res[i] = NAN;
+  } else {
+    merge_with_own<D>(a, b, nitems, item, qhead, o0, m, l, acc, res);
+  }
+  store_out<D>(out, res);
+  if (t == 0) __hip_atomic_store(&a.tickets[b], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Separate merge of every multi-partition (sequence, kv head): one wave each.
-__global__ __launch_bounds__(kMergeThreads) void paged_decode_reduce_kernel(AttnArgs a) {
-  const int bh = blockIdx.x;
-  const int len = a.context_lens[bh / kKVHeads];
-  if (len <= 0) return;
+// Separate merge of every multi-item sequence: one workgroup per (sequence, group of 8 q
+// heads); thread t folds dims 2(t % 32), +1 of q head 8 (blockIdx % 4) + t / 32, loading
+// up to merge_batch(2) = 32 items' partials per round trip.
+__global__ __launch_bounds__(kMergeThreads) void paged_decode_merge_kernel(AttnArgs a, int w) {
+  const int b = blockIdx.x / kKVHeads;
+  const int qhead = kGroup * (blockIdx.x % kKVHeads) + threadIdx.x / 32;
+  const int o0 = 2 * (threadIdx.x % 32);
   int nblk;
-  const int nparts = partitions_of(len, a.max_blocks, a.partition_blocks, nblk);
-  if (nparts <= 1) return;
-  merge_partitions<false>(a, bh, nparts, threadIdx.x);
+  const int nitems = items_of(a.context_lens[b], a.max_blocks, w, nblk);
+  if (nitems <= 1) return;
+  float res[2];
+  merge_items<false, 2>(a, b, nitems, qhead, o0, res);
+  store_out<2>(a.out + (static_cast<int64_t>(b) * kQHeads + qhead) * kHeadDim + o0, res);
 }
+
 // ---------------------------------------------------------------------------------------
 // Host-side validation and workspace layout.
 // ---------------------------------------------------------------------------------------
 
-int max_partitions(int32_t max_blocks, int32_t partition_blocks) {
+int max_items(int32_t max_blocks, int32_t partition_blocks) {
   return (max_blocks + partition_blocks - 1) / partition_blocks;
 }
+
+bool valid_partition(int32_t p) { return p == 1 || p == 2 || p == 4 || p == 8; }
 
 int check_attn_shape(int32_t batch, int32_t max_blocks, int32_t partition_blocks) {
   if (batch < 0 || batch > (1 << 20)) return set_error(PC_ERR_ARGUMENT, "batch %d out of range", batch);
   if (max_blocks < 1 || max_blocks > (1 << 16)) {
     return set_error(PC_ERR_ARGUMENT, "max_blocks %d out of range [1, 65536]", max_blocks);
   }
-  if (partition_blocks < 1 || partition_blocks > kMaxPartitionBlocks) {
-    return set_error(PC_ERR_ARGUMENT, "partition_blocks %d outside [1, %d]", partition_blocks,
-                     kMaxPartitionBlocks);
+  if (!valid_partition(partition_blocks)) {
+    return set_error(PC_ERR_ARGUMENT, "partition_blocks %d is not 1, 2, 4 or 8", partition_blocks);
   }
-  const int64_t grid = static_cast<int64_t>(batch) * kKVHeads * max_partitions(max_blocks, partition_blocks);
+  const int64_t grid = static_cast<int64_t>(batch) * max_items(max_blocks, partition_blocks);
   if (grid > INT32_MAX) return set_error(PC_ERR_ARGUMENT, "attention grid too large");
   return PC_OK;
 }
@@ -624,15 +665,20 @@ struct WorkspaceLayout {
 
 WorkspaceLayout workspace_layout(int32_t batch, int32_t max_blocks, int32_t partition_blocks) {
   auto round_up = [](int64_t x) { return (x + 255) / 256 * 256; };
-  const int64_t rows = static_cast<int64_t>(batch) * kQHeads * max_partitions(max_blocks, partition_blocks);
+  const int64_t items = static_cast<int64_t>(batch) * max_items(max_blocks, partition_blocks);
   WorkspaceLayout w;
   w.out_offset = 0;
-  w.ml_offset = round_up(rows * kHeadDim * 4);
-  w.bytes = w.ml_offset + round_up(rows * 2 * 4);
+  w.ml_offset = round_up(items * kItemOutputs * 4);
+  w.bytes = w.ml_offset + round_up(items * kQHeads * 2 * 4);
   return w;
 }
 
 bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+
+template <int W>
+void launch_items(const AttnArgs& a, unsigned grid, hipStream_t s) {
+  hipLaunchKernelGGL(paged_decode_item_kernel<W>, dim3(grid), dim3(64 * W), 0, s, a);
+}
 
 }  // namespace
 
@@ -651,23 +697,61 @@ int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t parti
 
 int64_t pc_attn_plan_capacity(int32_t batch, int32_t max_blocks, int32_t partition_blocks) {
   if (check_attn_shape(batch, max_blocks, partition_blocks) != PC_OK) return -1;
-  return static_cast<int64_t>(batch) * max_partitions(max_blocks, partition_blocks);
+  return static_cast<int64_t>(batch) * max_items(max_blocks, partition_blocks);
 }
 
-int32_t pc_attn_plan(const int32_t* context_lens, int32_t batch, int32_t max_blocks,
-                     int32_t partition_blocks, int32_t* work_items, int64_t capacity) {
+int32_t pc_attn_plan_record_ints(int32_t partition_blocks) {
+  if (!valid_partition(partition_blocks)) {
+    return -set_error(PC_ERR_ARGUMENT, "partition_blocks %d is not 1, 2, 4 or 8", partition_blocks);
+  }
+  return plan_fields(partition_blocks);
+}
+
+int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, int32_t batch,
+                     int32_t max_blocks, int32_t partition_blocks, int32_t* work_items, int64_t capacity) {
   if (int rc = check_attn_shape(batch, max_blocks, partition_blocks)) return -rc;
-  if (batch > 0 && (!context_lens || !work_items)) return -set_error(PC_ERR_ARGUMENT, "null pointer");
-  int64_t n = 0;
+  if (batch > 0 && (!context_lens || !block_tables || !work_items)) {
+    return -set_error(PC_ERR_ARGUMENT, "null pointer");
+  }
+  const int fields = plan_fields(partition_blocks);
+  int64_t total = 0;
   for (int32_t b = 0; b < batch; ++b) {
     const int32_t len = context_lens[b];
-    if (len <= 0) continue;
-    const int32_t nblk = static_cast<int32_t>(std::min<int64_t>((static_cast<int64_t>(len) + kSlots - 1) / kSlots, max_blocks));
-    const int32_t parts = max_partitions(nblk, partition_blocks);
-    if (n + parts > capacity) return -set_error(PC_ERR_ARGUMENT, "work item capacity %lld too small", static_cast<long long>(capacity));
-    for (int32_t p = 0; p < parts; ++p, ++n) {
-      work_items[2 * n] = b;
-      work_items[2 * n + 1] = p;
+    if (len > 0) total += max_items(std::min((len - 1) / kSlots + 1, max_blocks), partition_blocks);
+  }
+  if (total > capacity) {
+    return -set_error(PC_ERR_ARGUMENT, "work item capacity %lld too small (%lld items)",
+                      static_cast<long long>(capacity), static_cast<long long>(total));
+  }
+  // Workgroups are dispatched in record order. A multi-item sequence's closer -- its last
+  // item, the one with the fewest blocks -- goes after every other item of every
+  // sequence, so when it finishes its own blocks its siblings have long published their
+  // partials; before the closers, items with fewer blocks go later.
+  int64_t n = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    const bool closers = pass == 1;
+    for (int32_t count = partition_blocks; count >= 1; --count) {
+      for (int32_t b = 0; b < batch; ++b) {
+        const int32_t len = context_lens[b];
+        if (len <= 0) continue;
+        const int32_t nblk = std::min((len - 1) / kSlots + 1, max_blocks);
+        const int32_t items = max_items(nblk, partition_blocks);
+        const int32_t* row = block_tables + static_cast<int64_t>(b) * max_blocks;
+        for (int32_t i = 0; i < items; ++i) {
+          const bool closer = items > 1 && i == items - 1;
+          if (closer != closers || std::min(nblk - i * partition_blocks, partition_blocks) != count) continue;
+          int32_t* rec = work_items + n * fields;
+          rec[0] = b;
+          rec[1] = i;
+          rec[2] = len;
+          rec[3] = closer ? 1 : 0;
+          for (int32_t j = 0; j < fields - kPlanHeader; ++j) {
+            const int32_t blk = i * partition_blocks + j;
+            rec[kPlanHeader + j] = (j < count) ? row[blk] : 0;
+          }
+          ++n;
+        }
+      }
     }
   }
   ok();
@@ -741,9 +825,9 @@ int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t
   if (layer < 0 || layer >= kLayers) return set_error(PC_ERR_ARGUMENT, "layer %d outside [0, 22)", layer);
   if (int rc = check_attn_shape(batch, max_blocks, partition_blocks)) return rc;
   if (flags & ~PC_ATTN_SEPARATE_REDUCE) return set_error(PC_ERR_ARGUMENT, "unknown flags 0x%x", flags);
-  const int parts = max_partitions(max_blocks, partition_blocks);
-  if (parts > 1 && !workspace) return set_error(PC_ERR_ARGUMENT, "workspace required");
-  if (parts > 1 && !(flags & PC_ATTN_SEPARATE_REDUCE) && !tickets) {
+  const int items = max_items(max_blocks, partition_blocks);
+  if (items > 1 && !workspace) return set_error(PC_ERR_ARGUMENT, "workspace required");
+  if (items > 1 && !(flags & PC_ATTN_SEPARATE_REDUCE) && !tickets) {
     return set_error(PC_ERR_ARGUMENT, "tickets required for the fused merge");
   }
   if (!aligned(query, 16) || !aligned(out, 16) || !aligned(pool, 16) || !aligned(workspace, 256) ||
@@ -751,8 +835,8 @@ int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t
     return set_error(PC_ERR_ARGUMENT,
                      "query/out/pool must be 16-byte, tickets/work_items 4-byte, workspace 256-byte aligned");
   }
-  if (work_items && (num_work_items < 0 || num_work_items > static_cast<int64_t>(batch) * parts)) {
-    return set_error(PC_ERR_ARGUMENT, "num_work_items %d outside [0, batch * partitions]", num_work_items);
+  if (work_items && (num_work_items < 0 || num_work_items > static_cast<int64_t>(batch) * items)) {
+    return set_error(PC_ERR_ARGUMENT, "num_work_items %d outside [0, batch * items]", num_work_items);
   }
   if (batch == 0 || (work_items && num_work_items == 0)) return ok();
   const WorkspaceLayout w = workspace_layout(batch, max_blocks, partition_blocks);
@@ -771,18 +855,22 @@ int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t
   a.layer = layer;
   a.max_blocks = max_blocks;
   a.batch = batch;
-  a.partition_blocks = partition_blocks;
-  a.max_parts = parts;
+  a.max_items = items;
   a.fused_merge = (flags & PC_ATTN_SEPARATE_REDUCE) ? 0 : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
-  const unsigned grid = static_cast<unsigned>(work_items ? static_cast<int64_t>(num_work_items) : static_cast<int64_t>(batch) * parts) * kKVHeads;
-  hipLaunchKernelGGL(paged_decode_partition_kernel, dim3(grid), dim3(kAttnThreads), 0, s, a);
-  if (int rc = check_launch("paged_decode_partition")) return rc;
-  if (parts > 1 && !a.fused_merge) {
-    hipLaunchKernelGGL(paged_decode_reduce_kernel, dim3(static_cast<unsigned>(batch) * kKVHeads),
-                       dim3(kMergeThreads), 0, s, a);
-    return check_launch("paged_decode_reduce");
+  const unsigned grid = static_cast<unsigned>(work_items ? static_cast<int64_t>(num_work_items) : static_cast<int64_t>(batch) * items);
+  switch (partition_blocks) {
+    case 1: launch_items<1>(a, grid, s); break;
+    case 2: launch_items<2>(a, grid, s); break;
+    case 4: launch_items<4>(a, grid, s); break;
+    default: launch_items<8>(a, grid, s); break;
+  }
+  if (int rc = check_launch("paged_decode_item")) return rc;
+  if (items > 1 && !a.fused_merge) {
+    hipLaunchKernelGGL(paged_decode_merge_kernel, dim3(static_cast<unsigned>(batch) * kKVHeads),
+                       dim3(kMergeThreads), 0, s, a, static_cast<int>(partition_blocks));
+    return check_launch("paged_decode_merge");
   }
   return PC_OK;
 }

@@ -108,11 +108,12 @@ class _HostOnlyWriter:
 
 @dataclass(slots=True)
 class _DecodeBatch:
-    """Device block tables and lengths of one batch of requests, plus the host lengths
+    """Device block tables and lengths of one batch of requests, plus their host copies
     and the per-partition-size decode plans built from them."""
 
     tables: Tensor
     lengths: Tensor
+    host_tables: np.ndarray
     host_lengths: np.ndarray
     plans: Dict[int, Tensor]
 
@@ -430,13 +431,13 @@ class KVAllocator:
     def decode_work_items(
         self, request_ids: Sequence[RequestId], *, layer_index: int, partition_blocks: int
     ) -> Tensor:
-        """Device decode plan (int32 [items, 2] (row, partition) pairs) for the batch that
-        gather_block_tables returns, built once per allocator state and partition size
-        from the host lengths, so the 22 layers of a decode step share it."""
+        """Device decode plan (pc_attn_plan records: row, item, length, block ids) for the
+        batch that gather_block_tables returns, built once per allocator state and
+        partition size from the host tables, so the 22 layers of a decode step share it."""
         batch = self._gather(request_ids, layer_index)
         items = batch.plans.get(partition_blocks)
         if items is None:
-            plan = _hip.plan_work_items(batch.host_lengths, int(batch.tables.shape[1]), partition_blocks)
+            plan = _hip.plan_work_items(batch.host_lengths, batch.host_tables, partition_blocks)
             items = torch.from_numpy(plan).to(self._pool.device)
             batch.plans[partition_blocks] = items
         return items
@@ -463,6 +464,7 @@ class KVAllocator:
         result = _DecodeBatch(
             torch.from_numpy(tables).to(self._pool.device),
             torch.from_numpy(lengths).to(self._pool.device),
+            tables,
             lengths,
             {},
         )

@@ -205,7 +205,7 @@ def test_config1_golden_through_the_c_abi(device):
     out = torch.empty(1, 32, 64, dtype=torch.float16, device=device)
     tables = torch.tensor([w.table], dtype=torch.int32, device=device)
     lens = torch.tensor([128], dtype=torch.int32, device=device)
-    for parts in (4, 8, 32):
+    for parts in (1, 2, 4, 8):
         out.fill_(float("nan"))
         _hip.paged_decode_attention(out, query, pool, w.layer, tables, lens, partition_blocks=parts)
         torch.cuda.synchronize()
@@ -238,7 +238,7 @@ def _oracle_rows(pool, layer, w, queries, rows):
     return out
 
 
-@pytest.mark.parametrize("parts", [1, 5, 16, 32, 64])
+@pytest.mark.parametrize("parts", [1, 2, 4, 8])
 def test_batched_decode_b64_matches_oracle(device, parts):
     """Batch 64, lengths U{1..2048}, fragmented tables over an 8192-block pool; every row
     against the oracle restatement and FP64, for several split-K partition sizes."""
@@ -271,16 +271,16 @@ def test_long_context_b256_full_length(device):
     tables = torch.from_numpy(w.tables).to(device)
     lens = torch.from_numpy(w.lengths).to(device)
     results = {}
-    for parts in (8, 32, 64):
+    for parts in (2, 4, 8):
         out = torch.empty_like(queries)
         _hip.paged_decode_attention(out, queries, pool, layer, tables, lens, partition_blocks=parts)
         results[parts] = out
     torch.cuda.synchronize()
-    for parts in (8, 64):
-        torch.testing.assert_close(results[parts], results[32], **TOL)
+    for parts in (2, 8):
+        torch.testing.assert_close(results[parts], results[4], **TOL)
     expected = _oracle_rows(pool, layer, w, queries, [0, 1, 127, 255])
     for b, (oracle, fp64) in expected.items():
-        got = results[32][b : b + 1].reshape(1, 32, 1, 64).cpu()
+        got = results[4][b : b + 1].reshape(1, 32, 1, 64).cpu()
         torch.testing.assert_close(got, oracle, **TOL)
         torch.testing.assert_close(got, fp64, **TOL)
 
@@ -294,10 +294,10 @@ def test_fused_merge_equals_separate_reduce_and_rearms_tickets(device):
     queries = torch.from_numpy(w.queries(7)).to(device)
     tables = torch.from_numpy(w.tables).to(device)
     lens = torch.from_numpy(w.lengths).to(device)
-    for parts in (3, 8, 32):
+    for parts in (1, 4, 8):
         nbytes = _hip.workspace_bytes(w.batch, tables.shape[1], parts)
         workspace = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=device)  # scratch: contents irrelevant
-        tickets = torch.zeros(w.batch * 4, dtype=torch.int32, device=device)
+        tickets = torch.zeros(w.batch, dtype=torch.int32, device=device)
         separate = torch.empty_like(queries)
         _hip.paged_decode_attention(separate, queries, pool, 7, tables, lens, partition_blocks=parts, workspace=workspace, tickets=tickets, separate_reduce=True)
         for _ in range(3):
@@ -334,8 +334,8 @@ def test_planned_grid_equals_full_grid(device, separate):
     queries = torch.from_numpy(w.queries(9)).to(device)
     tables = torch.from_numpy(w.tables).to(device)
     lens = torch.from_numpy(lengths).to(device)
-    for parts in (1, 4, 16, 64):
-        items = torch.from_numpy(_hip.plan_work_items(lengths, tables.shape[1], parts)).to(device)
+    for parts in (1, 2, 4, 8):
+        items = torch.from_numpy(_hip.plan_work_items(lengths, w.tables, parts)).to(device)
         full = torch.full_like(queries, float("nan"))
         _hip.paged_decode_attention(full, queries, pool, 9, tables, lens, partition_blocks=parts, separate_reduce=separate)
         planned = torch.full_like(queries, float("nan"))
@@ -367,7 +367,7 @@ def test_cached_scratch_survives_changing_shapes(device):
     """Calls of different batch sizes, table widths and partition sizes share the cached
     per-stream scratch; each must still match the oracle."""
     pool = _random_pool(device, 1024, 17)
-    for batch, hi, parts, layer in ((3, 300, 4, 1), (9, 1000, 7, 2), (2, 2048, 1, 3), (9, 900, 32, 4)):
+    for batch, hi, parts, layer in ((3, 300, 4, 1), (9, 1000, 2, 2), (2, 2048, 1, 3), (9, 900, 8, 4)):
         w = workloads.batched_decode(batch=batch, lo=20, hi=hi, num_blocks=1024, seed=batch + hi)
         queries = torch.from_numpy(w.queries(layer)).to(device)
         out = torch.full_like(queries, float("nan"))
