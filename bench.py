@@ -4,14 +4,15 @@ Workload (the metric's configuration): batched one-token paged decode attention,
 32 query / 4 KV heads, head dim 64, fp16 KV with N(0,1) values, context lengths drawn
 uniformly from 1..2048 (partial last blocks included), fragmented block tables carved from
 a random permutation of an 8192-block pool, repeated over the pool's 22 layers. A step is
-one pass over the 22 layers (one attention launch per layer; split-K partitions are
-merged inside the same launch), with inputs
+one pass over the 22 layers (one pc_paged_decode_attn call per layer: the split-K item
+kernel, then the kernel that merges the items of multi-item sequences), with inputs
 resident in HBM; the 22 layer planes (1.48 GB of KV per step) exceed the 256 MB Infinity
 Cache, so the bytes come from HBM.
 
 Printed as one JSON line: value = algorithmic HBM bytes per step x steps / wall time
-(GB/s), plus decode tokens/s, the roofline of the partition kernel (per-launch HIP-event
-timing), and the CPU baseline (the oracle's op-for-op restatement of the reference's
+(GB/s), plus decode tokens/s, the roofline of the attention call (algorithmic bytes per
+call over the average call duration in the timed region; HBM traffic per call from the
+committed rocprofv3 counter summary), and the CPU baseline (the oracle's op-for-op restatement of the reference's
 torch CPU path, timed on a bounded sample on this host's cores).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
@@ -95,24 +96,6 @@ class DecodeLayers:
         for layer in range(LAYERS):
             self.launch(layer, stream)
 
-    def timed_launches(self, steps: int) -> float:
-        """Mean duration (ms) of one layer's attention launch, from HIP events recorded
-        around each launch on the launch stream."""
-        stream = torch.cuda.current_stream(self.device)
-        handle = stream.cuda_stream
-        times = []
-        for _ in range(steps):
-            marks = []
-            for layer in range(LAYERS):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                self.launch(layer, handle)
-                e1.record(stream)
-                marks.append((e0, e1))
-            torch.cuda.synchronize(self.device)
-            times.extend(e0.elapsed_time(e1) for e0, e1 in marks)
-        return float(np.mean(times))
-
 
 def run_decode(
     steps: int, warmup: int, partition_blocks: int, use_graph: bool = True,
@@ -159,7 +142,11 @@ def run_decode(
     total_ms = start.elapsed_time(stop)
     if not torch.equal(layers.out, eager_out):
         raise RuntimeError("timed steps produced different outputs than the warmup")
-    launch_ms = layers.timed_launches(steps=5)
+    # The timed region holds steps x 22 pc_paged_decode_attn calls back to back on one
+    # stream (item kernel, then merge kernel, no host work in between when replayed as a
+    # graph), so its HIP-event time divided by the call count is the average call
+    # duration; rocprofv3's per-kernel averages of the two kernels add up to it.
+    launch_ms = total_ms / (steps * LAYERS)
     return {
         "layers": layers,
         "w": w,
@@ -177,39 +164,78 @@ def run_decode(
 def cpu_baseline(layers: DecodeLayers, seconds: float) -> dict:
     """The oracle's op-for-op restatement of the reference torch CPU path
     (attention.py:14-53, one call per sequence as in decoder.py:182-190), run over whole
-    layers of the same workload until ~`seconds` of CPU work, on all of this host's cores.
-    Only the attention calls are timed (copying each layer's blocks to host memory is not)."""
+    layers of the same workload -- cycling through the 22 layers again if needed -- until
+    ~`seconds` of CPU work, on all of this host's cores. Only the attention calls are timed
+    (copying each layer's blocks to host memory is not)."""
     from oracle import paged_reference as ref
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     w = layers.w
     host_tables = [w.tables[b, : (int(w.lengths[b]) + 15) // 16].tolist() for b in range(w.batch)]
+    used = sorted({blk for table in host_tables for blk in table})
+    remap = {blk: i for i, blk in enumerate(used)}
+    index = torch.tensor(used, dtype=torch.long, device=layers.device)
+    local_tables = [[remap[x] for x in table] for table in host_tables]
     done_bytes, done_layers, elapsed = 0, 0, 0.0
-    for layer in range(LAYERS):
-        used = sorted({blk for table in host_tables for blk in table})
-        remap = {blk: i for i, blk in enumerate(used)}
-        index = torch.tensor(used, dtype=torch.long, device=layers.device)
+    while elapsed < seconds:
+        layer = done_layers % LAYERS
         sub = torch.empty((LAYERS, 2, len(used), 16, 4, 64), dtype=torch.float16)
         sub[layer] = layers.pool[layer].index_select(1, index).cpu()
         queries = layers.queries[layer].reshape(w.batch, 1, 32, 1, 64).cpu()
         start = time.perf_counter()
         for b in range(w.batch):
-            ref.reference_paged_attention(queries[b], sub, layer, [remap[x] for x in host_tables[b]], int(w.lengths[b]))
+            ref.reference_paged_attention(queries[b], sub, layer, local_tables[b], int(w.lengths[b]))
         elapsed += time.perf_counter() - start
         done_bytes += attention_bytes(w.lengths)
         done_layers += 1
-        if elapsed >= seconds:
-            break
     return {
         "value": round(done_bytes / elapsed / 1e9, 4),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"{done_layers} of 22 layers x all {w.batch} sequences of the same workload, one reference "
-        f"paged_attention call per sequence, {elapsed:.1f} s of CPU time; decode tokens/s at that rate "
-        f"{w.batch * done_layers / LAYERS / elapsed:.2f}",
+        "sample": f"{done_layers} layer passes (cycling through the 22 layers) x all {w.batch} sequences of the "
+        f"same workload, one reference paged_attention call per sequence, {elapsed:.1f} s of CPU time on "
+        f"{cores} threads; decode tokens/s at that rate {w.batch * done_layers / LAYERS / elapsed:.2f}",
     }
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_decode_attention_b64_hbm_traffic.txt")
+
+
+def measured_traffic(partition_blocks: int, merge: str) -> int | None:
+    """HBM bytes per attention call (item + merge kernels) from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary, scaled by the plain-copy calibration recorded there;
+    None unless that summary was made for this library version and configuration."""
+    try:
+        with open(TRAFFIC_FILE) as handle:
+            fields = dict(
+                line.split(":", 1) for line in handle.read().splitlines() if line.count(":") >= 1 and not line.startswith(" ")
+            )
+    except OSError:
+        return None
+    fields = {k.strip(): v.strip() for k, v in fields.items()}
+    try:
+        same = (
+            int(fields["abi_version"]) == _hip.ABI_VERSION
+            and int(fields["partition_blocks"]) == partition_blocks
+            and fields["merge"] == merge
+        )
+        return int(fields["traffic_bytes_per_call"]) if same else None
+    except (KeyError, ValueError):
+        return None
+
+
+def calibration_copy(mib: int, device: torch.device) -> None:
+    """One plain device-to-device copy of `mib` MiB (torch's elementwise copy kernel),
+    outside any timed region: under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE give the
+    counters' scale for a known number of bytes."""
+    src = torch.ones(mib * 2**20 // 4, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize(device)
+    dst.copy_(src)
+    torch.cuda.synchronize(device)
+    del src, dst
 
 
 def main() -> int:
@@ -223,6 +249,8 @@ def main() -> int:
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-graph", action="store_true", help="launch from Python instead of replaying a HIP graph")
+    parser.add_argument("--calibrate-copy-mib", type=int, default=0,
+                        help="run one plain copy of this many MiB first (counter calibration under rocprofv3 --pmc)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(
@@ -233,13 +261,15 @@ def main() -> int:
         return 2
 
     torch.cuda.set_device(0)
+    if args.calibrate_copy_mib > 0:
+        calibration_copy(args.calibrate_copy_mib, torch.device("cuda:0"))
     parts = args.partition_blocks or _hip.default_partition_blocks()
     r = run_decode(args.steps, args.warmup, parts, use_graph=not args.no_graph, separate_reduce=args.merge == "separate")
     w, layers = r["w"], r["layers"]
     print(
         f"workload: batch {w.batch}, sum of lengths {int(w.lengths.sum())}, {r['bytes_per_launch'] / 1e6:.1f} MB per layer; "
         f"step {r['ms_per_step']:.3f} ms ({'graph' if r['graph'] else 'eager'}), {r['gbps']:.0f} GB/s, "
-        f"{r['tokens_per_s']:.0f} tok/s; one layer's launch {r['launch_ms'] * 1e3:.1f} us ({r['launch_gbps']:.0f} GB/s)",
+        f"{r['tokens_per_s']:.0f} tok/s; one attention call {r['launch_ms'] * 1e3:.1f} us ({r['launch_gbps']:.0f} GB/s)",
         file=sys.stderr,
         flush=True,
     )
@@ -277,14 +307,14 @@ def main() -> int:
         "decode_tokens_per_s": round(r["tokens_per_s"], 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "pc_paged_decode_attn: paged_decode_partition_kernel"
-            + (" + paged_decode_reduce_kernel" if args.merge == "separate" else " (fused merge)"),
+            "kernel": "pc_paged_decode_attn: paged_decode_item_kernel"
+            + (" + paged_decode_merge_kernel" if args.merge == "separate" else " (fused closer merge)"),
             "achieved": round(r["launch_gbps"], 2),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(r["launch_gbps"] / PEAK_HBM_GBPS, 4),
-            "traffic": None,
-            "avg_launch_us": round(r["launch_ms"] * 1e3, 3),
+            "traffic": measured_traffic(parts, args.merge),
+            "avg_call_us": round(r["launch_ms"] * 1e3, 3),
             "bytes_per_launch": r["bytes_per_launch"],
         },
         "cpu_baseline": baseline,

@@ -386,13 +386,15 @@ __device__ __forceinline__ void store_out(_Float16* dst, const float (&v)[D]) {
   }
 }
 
-template <int W>
+template <int W, bool kPlanned>
 __global__ __launch_bounds__(64 * W) void paged_decode_item_kernel(AttnArgs a) {
   constexpr int D = kItemOutputs / (64 * W);  // outputs per thread in the workgroup merge
   __shared__ __attribute__((aligned(16))) char lds[W * kWaveLds];
   __shared__ int32_t ticket_slot;
 
-  const int wave = threadIdx.x >> 6;
+  // Wave index as a scalar, so every per-wave address below is scalar arithmetic and the
+  // block-id loads are scalar loads.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int c = lane & 15;
   const int g = lane >> 4;
@@ -401,20 +403,24 @@ __global__ __launch_bounds__(64 * W) void paged_decode_item_kernel(AttnArgs a) {
   int32_t id;
   bool closer;  // merges the sequence's items (fused merge)
   const int blk_in_item = wave;
-  if (a.work_items) {
-    // Planned grid: one workgroup per item that exists. Its plan record (one uniform
-    // load) carries the sequence, the item, the context length and the item's block ids,
-    // so the KV loads leave after a single round trip.
+  if constexpr (kPlanned) {
+    // Planned grid: one workgroup per item that exists. The record header and this
+    // wave's block id are requested together, before any branch, so the KV loads leave
+    // after a single round trip.
     const int32_t* rec = a.work_items + static_cast<int64_t>(blockIdx.x) * plan_fields(W);
-    b = rec[0];
-    item = rec[1];
-    len = rec[2];
-    closer = rec[3] != 0;
+    const int4 hdr = *reinterpret_cast<const int4*>(rec);
     id = rec[kPlanHeader + blk_in_item];
-    if (static_cast<uint32_t>(b) >= static_cast<uint32_t>(a.batch) ||
-        static_cast<uint32_t>(item) >= static_cast<uint32_t>(a.max_items)) {
-      return;
-    }
+    // A record outside the batch or the workspace is skipped at the item check below; it
+    // is clamped, not branched on, here so that no load waits behind the check.
+    const bool in_range = static_cast<uint32_t>(hdr.x) < static_cast<uint32_t>(a.batch) &&
+                          static_cast<uint32_t>(hdr.y) < static_cast<uint32_t>(a.max_items);
+    b = in_range ? hdr.x : 0;
+    item = in_range ? hdr.y : a.max_items;
+    len = hdr.z;
+    closer = hdr.w != 0;
+    // The block id is consumed here so that its load leaves with the header's instead
+    // of after the item check below.
+    asm volatile("" ::"s"(id));
   } else {
     // Full grid: item slots past a sequence's length exit below; the length and this
     // wave's block id come from the device tables in one round trip.
@@ -435,7 +441,7 @@ __global__ __launch_bounds__(64 * W) void paged_decode_item_kernel(AttnArgs a) {
   int nblk;
   const int nitems = items_of(len, a.max_blocks, W, nblk);
   if (item >= nitems) return;  // uniform over the workgroup
-  if (!a.work_items) closer = item == nitems - 1;  // the sequence's highest workgroup index
+  if constexpr (!kPlanned) closer = item == nitems - 1;  // the sequence's highest workgroup index
   const bool active = blk < nblk;  // uniform over the wave; wave 0 is always active
 
   char* vl = lds + wave * kWaveLds;
@@ -677,7 +683,11 @@ bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p
 
 template <int W>
 void launch_items(const AttnArgs& a, unsigned grid, hipStream_t s) {
-  hipLaunchKernelGGL(paged_decode_item_kernel<W>, dim3(grid), dim3(64 * W), 0, s, a);
+  if (a.work_items) {
+    hipLaunchKernelGGL((paged_decode_item_kernel<W, true>), dim3(grid), dim3(64 * W), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((paged_decode_item_kernel<W, false>), dim3(grid), dim3(64 * W), 0, s, a);
+  }
 }
 
 }  // namespace
