@@ -54,14 +54,7 @@ def attention_bytes(lengths: np.ndarray) -> int:
 class DecodeLayers:
     """Device buffers and raw C-ABI launches for the 22-layer decode step."""
 
-    def __init__(
-        self,
-        w: workloads.BatchedDecode,
-        device: torch.device,
-        partition_blocks: int,
-        seed: int,
-        separate_reduce: bool = _hip.DEFAULT_SEPARATE_REDUCE,
-    ) -> None:
+    def __init__(self, w: workloads.BatchedDecode, device: torch.device, seed: int) -> None:
         gen = torch.Generator(device=device).manual_seed(seed)
         self.w = w
         self.device = device
@@ -70,23 +63,19 @@ class DecodeLayers:
         self.out = torch.empty_like(self.queries)
         self.tables = torch.from_numpy(w.tables).to(device)
         self.lens = torch.from_numpy(w.lengths).to(device)
-        self.parts = partition_blocks
-        self.flags = _hip.SEPARATE_REDUCE if separate_reduce else 0
         self.lib = _hip.load()
         self.max_blocks = int(w.tables.shape[1])
-        nbytes = int(self.lib.pc_attn_workspace_bytes(w.batch, self.max_blocks, partition_blocks))
-        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
-        self.tickets = torch.zeros(w.batch, dtype=torch.int32, device=device)
+        nbytes = int(self.lib.pc_attn_workspace_bytes(w.batch, self.max_blocks))
+        self.workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
         # One decode plan per step, shared by the 22 layers (built from the host lengths,
         # like the block tables).
-        self.items = torch.from_numpy(_hip.plan_work_items(w.lengths, w.tables, partition_blocks)).to(device)
+        self.plan = torch.from_numpy(_hip.decode_plan(w.lengths, w.tables)).to(device)
 
     def launch(self, layer: int, stream: int) -> None:
         status = self.lib.pc_paged_decode_attn(
             self.out[layer].data_ptr(), self.queries[layer].data_ptr(), self.pool.data_ptr(), self.w.num_blocks,
-            layer, self.tables.data_ptr(), self.max_blocks, self.lens.data_ptr(), self.w.batch, self.parts,
-            self.items.data_ptr(), self.items.shape[0], self.workspace.data_ptr(), self.tickets.data_ptr(),
-            self.flags, stream,
+            layer, self.lens.data_ptr(), self.w.batch, self.max_blocks, self.plan.data_ptr(), self.plan.shape[0],
+            self.workspace.data_ptr(), stream,
         )
         if status:
             raise RuntimeError(self.lib.pc_last_error().decode())
@@ -97,14 +86,11 @@ class DecodeLayers:
             self.launch(layer, stream)
 
 
-def run_decode(
-    steps: int, warmup: int, partition_blocks: int, use_graph: bool = True,
-    separate_reduce: bool = _hip.DEFAULT_SEPARATE_REDUCE,
-) -> dict:
+def run_decode(steps: int, warmup: int, use_graph: bool = True) -> dict:
     """Times `steps` 22-layer decode steps of the batch-64 workload; returns the figures."""
     device = torch.device("cuda:0")
     w = workloads.batched_decode(batch=64, num_blocks=8192)
-    layers = DecodeLayers(w, device, partition_blocks, seed=1234, separate_reduce=separate_reduce)
+    layers = DecodeLayers(w, device, seed=1234)
     bytes_per_launch = attention_bytes(w.lengths)
     for _ in range(warmup):
         layers.step()
@@ -203,10 +189,10 @@ def cpu_baseline(layers: DecodeLayers, seconds: float) -> dict:
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_decode_attention_b64_hbm_traffic.txt")
 
 
-def measured_traffic(partition_blocks: int, merge: str) -> int | None:
+def measured_traffic() -> int | None:
     """HBM bytes per attention call (item + merge kernels) from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary, scaled by the plain-copy calibration recorded there;
-    None unless that summary was made for this library version and configuration."""
+    None unless that summary was made for this library version."""
     try:
         with open(TRAFFIC_FILE) as handle:
             fields = dict(
@@ -216,11 +202,7 @@ def measured_traffic(partition_blocks: int, merge: str) -> int | None:
         return None
     fields = {k.strip(): v.strip() for k, v in fields.items()}
     try:
-        same = (
-            int(fields["abi_version"]) == _hip.ABI_VERSION
-            and int(fields["partition_blocks"]) == partition_blocks
-            and fields["merge"] == merge
-        )
+        same = int(fields["abi_version"]) == _hip.ABI_VERSION
         return int(fields["traffic_bytes_per_call"]) if same else None
     except (KeyError, ValueError):
         return None
@@ -243,9 +225,6 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--partition-blocks", type=int, default=None)
-    parser.add_argument("--merge", choices=("separate", "fused"), default="separate" if _hip.DEFAULT_SEPARATE_REDUCE else "fused",
-                        help="merge split-K partitions in a second kernel or in the last partition wave")
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-graph", action="store_true", help="launch from Python instead of replaying a HIP graph")
@@ -263,8 +242,7 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.calibrate_copy_mib > 0:
         calibration_copy(args.calibrate_copy_mib, torch.device("cuda:0"))
-    parts = args.partition_blocks or _hip.default_partition_blocks()
-    r = run_decode(args.steps, args.warmup, parts, use_graph=not args.no_graph, separate_reduce=args.merge == "separate")
+    r = run_decode(args.steps, args.warmup, use_graph=not args.no_graph)
     w, layers = r["w"], r["layers"]
     print(
         f"workload: batch {w.batch}, sum of lengths {int(w.lengths.sum())}, {r['bytes_per_launch'] / 1e6:.1f} MB per layer; "
@@ -298,8 +276,8 @@ def main() -> int:
             "layers": LAYERS,
             "pool_blocks": w.num_blocks,
             "sum_context_tokens": int(w.lengths.sum()),
-            "partition_blocks": parts,
-            "split_k_merge": "separate_kernel" if args.merge == "separate" else "fused_last_arriver",
+            "blocks_per_work_item": 9,
+            "split_k_merge": "separate_kernel",
             "kv_dtype": "f16",
             "launch": "hip_graph" if r["graph"] else "eager",
         },
@@ -307,13 +285,12 @@ def main() -> int:
         "decode_tokens_per_s": round(r["tokens_per_s"], 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "pc_paged_decode_attn: paged_decode_item_kernel"
-            + (" + paged_decode_merge_kernel" if args.merge == "separate" else " (fused closer merge)"),
+            "kernel": "pc_paged_decode_attn: paged_decode_item_kernel + paged_decode_merge_kernel",
             "achieved": round(r["launch_gbps"], 2),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(r["launch_gbps"] / PEAK_HBM_GBPS, 4),
-            "traffic": measured_traffic(parts, args.merge),
+            "traffic": measured_traffic(),
             "avg_call_us": round(r["launch_ms"] * 1e3, 3),
             "bytes_per_launch": r["bytes_per_launch"],
         },

@@ -66,75 +66,55 @@ int pc_kv_append(void* pool, int64_t num_blocks, int32_t layer_begin, int32_t nu
  * Replaces the two page traversals of paged_attention
  * (reference src/pagedcore/attention.py:14-53) and the Python page generator that feeds
  * them, KVAllocator.iter_layer_blocks (reference src/pagedcore/kv_cache.py:248-270): the
- * block table is walked inside the kernel.
+ * plan lists each sequence's blocks and the kernels read them from the pool directly.
  *
  *   query        [batch][32][64] fp16, contiguous; q head h reads kv head h / 8
- *   out          [batch][32][64] fp16, contiguous, 16-byte aligned (query and pool too)
- *   block_tables [batch][max_blocks] int32 physical block ids (row b lists sequence b's
- *                blocks in logical order; only the first ceil(len/16) are read)
- *   context_lens [batch] int32, each in [1, max_blocks * 16] (0 or less: row not written)
+ *   out          [batch][32][64] fp16, contiguous (query, out, pool and plan 16-byte aligned)
+ *   context_lens [batch] int32 device copy of the lengths the plan was built from
+ *                (0 or less: the row is not written)
+ *   plan         num_records records of pc_attn_plan_record_ints() int32 from pc_attn_plan()
+ *                for the same lengths and block tables (device copy); one plan serves every
+ *                layer of a decode step
  *   out[b][h] = softmax(q[b][h] . K[b][:len]^T / 8) . V[b][:len], computed in fp32 and
  *   rounded once to fp16. Slots past len are never multiplied, so poisoned (NaN) tail
  *   slots do not reach the output. A block id outside [0, num_blocks) is never
- *   dereferenced; its sequence's output rows become NaN.
+ *   dereferenced; its sequence's output rows become NaN. A plan that does not match
+ *   context_lens gives wrong rows, never an access outside the buffers.
  *
- * Split-K: a sequence's table is cut into work items of `partition_blocks` blocks (1, 2,
- * 4 or 8), one workgroup per item and one wave per block. A sequence covered by one item
- * is written directly; longer ones leave one partial per item in the workspace, merged
- * by a second kernel (flags = PC_ATTN_SEPARATE_REDUCE) or, flags = 0, by the last
- * workgroup of the sequence to finish (one launch).
- *   work_items  null: the grid covers batch * ceil(max_blocks / partition_blocks) item
- *               slots and the slots past a sequence's length exit at once; otherwise the
- *               host-built plan from pc_attn_plan() for the same context_lens,
- *               block_tables and partition_blocks (device copy, num_work_items records):
- *               the grid then holds only items that exist, and the item kernel takes
- *               block ids and lengths from the plan. A plan that does not match the
- *               tables gives wrong rows (never an out-of-pool read). One plan serves
- *               every layer of a decode step.
- *   workspace  fp32 partials, pc_attn_workspace_bytes() bytes, 256-byte aligned; scratch,
- *              nothing in it needs to survive between calls (unused, may be null, when
- *              max_blocks <= partition_blocks);
- *   tickets    int32 [batch], one merge ticket per sequence, only read by the fused merge:
- *              ZERO-FILLED BEFORE ITS FIRST USE; every call leaves the tickets at zero
- *              again, so one ticket array serves any number of later calls.
- * Calls that share a workspace or tickets must not overlap (use one set per stream).
+ * Split-K: a sequence is cut into work items of 9 blocks, one workgroup each. A sequence
+ * of one item is written directly; longer ones leave one fp32 partial per item and kv head
+ * in `workspace` (pc_attn_workspace_bytes() bytes, 256-byte aligned, scratch whose contents
+ * do not matter between calls; may be null when max_blocks <= 9), merged by a second kernel
+ * launched on the same stream. Calls that share a workspace must not overlap.
  */
-#define PC_ATTN_SEPARATE_REDUCE 1
-
-int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t num_blocks,
-                         int32_t layer, const int32_t* block_tables, int32_t max_blocks,
-                         const int32_t* context_lens, int32_t batch, int32_t partition_blocks,
-                         const int32_t* work_items, int32_t num_work_items, void* workspace,
-                         int32_t* tickets, int32_t flags, void* stream);
+int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t num_blocks, int32_t layer,
+                         const int32_t* context_lens, int32_t batch, int32_t max_blocks, const int32_t* plan,
+                         int32_t num_records, void* workspace, void* stream);
 
 /* Workspace size in bytes for pc_paged_decode_attn; 0 on invalid arguments. */
-int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t partition_blocks);
+int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks);
 
 /*
  * Host-side decode plan (no device access). context_lens [batch] and block_tables
- * [batch][max_blocks] are HOST copies of the tables the attention call will receive;
- * work_items is HOST memory. Writes one record of pc_attn_plan_record_ints() int32 per
- * work item that exists -- items of partition_blocks blocks first (sequence-major), then
- * the shorter tail items by descending block count, since workgroups are dispatched in
- * record order:
- *   {sequence, item, context length, 0, block ids of the item's partition_blocks blocks
- *    (0 past the sequence's last block), 0 padding}
- * and returns how many; returns -pc_status on invalid arguments or if `capacity` (in
- * records) is too small. pc_attn_plan_capacity() gives a capacity that always suffices
- * (-1 on invalid arguments). The kernel reads a record with one load, so the block
- * loads of a work item wait for one round trip instead of two.
+ * [batch][max_blocks] are HOST arrays (row b: sequence b's physical blocks in logical order,
+ * only the first ceil(len / 16) read); plan is HOST memory of `capacity` records. Writes one
+ * record of pc_attn_plan_record_ints() int32 per work item,
+ *   {sequence, item, context length, items of the sequence, 9 block ids (past the
+ *    sequence's last block: its last id), 0, 0, 0},
+ * dealing sequences (longest first) to 8 bins of balanced item counts so that all items of
+ * a sequence run on one XCD; bins are interleaved record by record and padded with records
+ * whose sequence is -1. Returns the record count, or -pc_status on invalid arguments or if
+ * `capacity` is too small; pc_attn_plan_capacity() always suffices (-1 on invalid
+ * arguments).
  *
  * Replaces nothing in the reference: PagedCore walks each sequence's pages in Python
  * (reference src/pagedcore/attention.py:31-53); the plan is what lets one launch cover a
- * ragged batch without idle workgroups.
+ * ragged batch with every block load issued at once.
  */
-int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, int32_t batch,
-                     int32_t max_blocks, int32_t partition_blocks, int32_t* work_items, int64_t capacity);
-int32_t pc_attn_plan_record_ints(int32_t partition_blocks);
-int64_t pc_attn_plan_capacity(int32_t batch, int32_t max_blocks, int32_t partition_blocks);
-
-/* Default blocks per work item (partition_blocks) used by the Python layer. */
-int32_t pc_attn_default_partition_blocks(void);
+int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, int32_t batch, int32_t max_blocks,
+                     int32_t* plan, int64_t capacity);
+int32_t pc_attn_plan_record_ints(void);
+int64_t pc_attn_plan_capacity(int32_t batch, int32_t max_blocks);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,7 @@ import numpy as np
 import torch
 from torch import Tensor
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 LIBRARY_NAME = "libpagedcore_hip.so"
 
 _lock = threading.Lock()
@@ -41,20 +41,18 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pc_abi_version.argtypes = []
     lib.pc_last_error.restype = ctypes.c_char_p
     lib.pc_last_error.argtypes = []
-    lib.pc_attn_default_partition_blocks.restype = _i32
-    lib.pc_attn_default_partition_blocks.argtypes = []
     lib.pc_attn_workspace_bytes.restype = _i64
-    lib.pc_attn_workspace_bytes.argtypes = [_i32, _i32, _i32]
+    lib.pc_attn_workspace_bytes.argtypes = [_i32, _i32]
     lib.pc_kv_append.restype = ctypes.c_int
     lib.pc_kv_append.argtypes = [_p, _i64, _i32, _i32, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _p]
     lib.pc_paged_decode_attn.restype = ctypes.c_int
-    lib.pc_paged_decode_attn.argtypes = [_p, _p, _p, _i64, _i32, _p, _i32, _p, _i32, _i32, _p, _i32, _p, _p, _i32, _p]
+    lib.pc_paged_decode_attn.argtypes = [_p, _p, _p, _i64, _i32, _p, _i32, _i32, _p, _i32, _p, _p]
     lib.pc_attn_plan.restype = _i32
-    lib.pc_attn_plan.argtypes = [_p, _p, _i32, _i32, _i32, _p, _i64]
+    lib.pc_attn_plan.argtypes = [_p, _p, _i32, _i32, _p, _i64]
     lib.pc_attn_plan_record_ints.restype = _i32
-    lib.pc_attn_plan_record_ints.argtypes = [_i32]
+    lib.pc_attn_plan_record_ints.argtypes = []
     lib.pc_attn_plan_capacity.restype = _i64
-    lib.pc_attn_plan_capacity.argtypes = [_i32, _i32, _i32]
+    lib.pc_attn_plan_capacity.argtypes = [_i32, _i32]
 
 
 def load() -> ctypes.CDLL:
@@ -92,10 +90,6 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def default_partition_blocks() -> int:
-    return int(load().pc_attn_default_partition_blocks())
-
-
 def kv_append(pool: Tensor, layer_begin: int, key: Tensor, value: Tensor, slot_mapping: Tensor) -> None:
     """pool[layer_begin + l, 0/1, slot // 16, slot % 16] = key/value[l, t] for slot = slot_mapping[t].
 
@@ -128,14 +122,7 @@ def kv_append(pool: Tensor, layer_begin: int, key: Tensor, value: Tensor, slot_m
     _check(lib, "pc_kv_append", status)
 
 
-SEPARATE_REDUCE = 1  # PC_ATTN_SEPARATE_REDUCE
-# Split-K partitions are merged by the separate merge kernel unless a caller asks for
-# the fused last-arriver merge: on MI355X the second launch costs less than making every
-# partition wave wait for its stores to be acknowledged before it takes a ticket.
-DEFAULT_SEPARATE_REDUCE = True
-
 _workspaces: Dict[Tuple[int, int], Tensor] = {}
-_tickets: Dict[Tuple[int, int], Tensor] = {}
 
 
 def _stream_key(device: torch.device) -> Tuple[int, int]:
@@ -155,28 +142,13 @@ def attention_workspace(device: torch.device, nbytes: int) -> Tensor:
     return workspace
 
 
-def merge_tickets(device: torch.device, batch: int) -> Tensor:
-    """Merge tickets (int32, one per sequence) for the current stream.
-
-    Zero-filled when created or grown; the kernel leaves every ticket at zero after each
-    call, so the array is reused as is.
-    """
-    key = _stream_key(device)
-    tickets = _tickets.get(key)
-    if tickets is None or tickets.numel() < batch:
-        tickets = torch.zeros(max(batch, 64), dtype=torch.int32, device=device)
-        _tickets[key] = tickets
-    return tickets
+def workspace_bytes(batch: int, max_blocks: int) -> int:
+    return int(load().pc_attn_workspace_bytes(batch, max_blocks))
 
 
-def workspace_bytes(batch: int, max_blocks: int, partition_blocks: int) -> int:
-    return int(load().pc_attn_workspace_bytes(batch, max_blocks, partition_blocks))
-
-
-def plan_work_items(context_lens: np.ndarray, block_tables: np.ndarray, partition_blocks: int) -> np.ndarray:
-    """Host decode plan: int32 [items, record_ints] records {sequence, item, context
-    length, 0, the item's block ids} for every work item that exists, computed by
-    pc_attn_plan from HOST copies of the lengths and block tables [batch, max_blocks]."""
+def decode_plan(context_lens: np.ndarray, block_tables: np.ndarray) -> np.ndarray:
+    """Host decode plan: int32 [records, pc_attn_plan_record_ints()] from pc_attn_plan, built
+    from HOST copies of the lengths [batch] and block tables [batch, max_blocks]."""
     lib = load()
     lens = np.ascontiguousarray(context_lens, dtype=np.int32)
     tables = np.ascontiguousarray(block_tables, dtype=np.int32)
@@ -184,16 +156,15 @@ def plan_work_items(context_lens: np.ndarray, block_tables: np.ndarray, partitio
     if tables.ndim != 2 or tables.shape[0] != batch:
         raise HipExtensionError("block_tables must be [batch, max_blocks] matching context_lens")
     max_blocks = int(tables.shape[1])
-    fields = int(lib.pc_attn_plan_record_ints(partition_blocks))
-    capacity = int(lib.pc_attn_plan_capacity(batch, max_blocks, partition_blocks))
-    if fields < 0 or capacity < 0:
+    fields = int(lib.pc_attn_plan_record_ints())
+    capacity = int(lib.pc_attn_plan_capacity(batch, max_blocks))
+    if capacity < 0:
         _check(lib, "pc_attn_plan_capacity", 1)
-    items = np.empty((max(capacity, 1), fields), dtype=np.int32)
-    count = int(lib.pc_attn_plan(lens.ctypes.data, tables.ctypes.data, batch, max_blocks, partition_blocks,
-                                 items.ctypes.data, capacity))
+    plan = np.empty((max(capacity, 1), fields), dtype=np.int32)
+    count = int(lib.pc_attn_plan(lens.ctypes.data, tables.ctypes.data, batch, max_blocks, plan.ctypes.data, capacity))
     if count < 0:
         _check(lib, "pc_attn_plan", -count)
-    return items[:count]
+    return plan[:count]
 
 
 def paged_decode_attention(
@@ -204,61 +175,47 @@ def paged_decode_attention(
     block_tables: Tensor,
     context_lens: Tensor,
     *,
-    partition_blocks: Optional[int] = None,
-    work_items: Optional[Tensor] = None,
+    plan: Optional[Tensor] = None,
     workspace: Optional[Tensor] = None,
-    tickets: Optional[Tensor] = None,
-    separate_reduce: Optional[bool] = None,
 ) -> None:
     """out[b] = paged decode attention of query[b] over layer `layer` of the pool.
 
-    out/query: fp16 [batch, 32, 64] contiguous; block_tables: int32 [batch, max_blocks]
-    contiguous; context_lens: int32 [batch]. All on the pool's device. `partition_blocks`
-    (1, 2, 4 or 8; None: the library default) is the number of blocks one workgroup
-    covers, one wave per block. `work_items`: the plan_work_items() rows for the same
-    lengths, table width and partition size, as a contiguous int32 device tensor (None:
-    full grid). `workspace` (uint8) and `tickets` (int32 [>= batch], zero-filled before
-    first use) default to per-stream cached buffers. `separate_reduce` None:
-    DEFAULT_SEPARATE_REDUCE.
+    out/query: fp16 [batch, 32, 64] contiguous; block_tables: int32 [batch, max_blocks];
+    context_lens: int32 [batch] contiguous. All on the pool's device. `plan`: the
+    decode_plan() rows for the same lengths and tables as a contiguous int32 device tensor
+    (None: built here from host copies, which synchronizes). `workspace` (uint8) defaults to
+    the per-stream cached buffer.
     """
-    if separate_reduce is None:
-        separate_reduce = DEFAULT_SEPARATE_REDUCE
     lib = load()
     batch, max_blocks = block_tables.shape
-    parts = partition_blocks if partition_blocks is not None else default_partition_blocks()
-    nbytes = int(lib.pc_attn_workspace_bytes(batch, max_blocks, parts))
+    nbytes = int(lib.pc_attn_workspace_bytes(batch, max_blocks))
     if nbytes <= 0:
-        raise HipExtensionError(f"invalid attention shape batch={batch} max_blocks={max_blocks} partition={parts}")
+        raise HipExtensionError(f"invalid attention shape batch={batch} max_blocks={max_blocks}")
     if workspace is None:
         workspace = attention_workspace(pool.device, nbytes)
     elif workspace.numel() * workspace.element_size() < nbytes:
         raise HipExtensionError(f"workspace needs {nbytes} bytes")
-    if tickets is None:
-        tickets = merge_tickets(pool.device, batch)
-    elif tickets.dtype != torch.int32 or tickets.numel() < batch:
-        raise HipExtensionError(f"tickets must be int32 with at least {batch} entries")
-    if work_items is not None and (
-        work_items.dtype != torch.int32 or work_items.dim() != 2
-        or work_items.shape[1] != int(lib.pc_attn_plan_record_ints(parts))
-        or not work_items.is_contiguous()
+    if plan is None:
+        plan = torch.from_numpy(decode_plan(context_lens.cpu().numpy(), block_tables.cpu().numpy())).to(pool.device)
+    if (
+        plan.dtype != torch.int32
+        or plan.dim() != 2
+        or plan.shape[1] != int(lib.pc_attn_plan_record_ints())
+        or not plan.is_contiguous()
     ):
-        raise HipExtensionError("work_items must be a contiguous int32 plan_work_items() array for this partition size")
+        raise HipExtensionError("plan must be a contiguous int32 decode_plan() array")
     status = lib.pc_paged_decode_attn(
         out.data_ptr(),
         query.data_ptr(),
         pool.data_ptr(),
         pool.shape[2],
         layer,
-        block_tables.data_ptr(),
-        max_blocks,
         context_lens.data_ptr(),
         batch,
-        parts,
-        work_items.data_ptr() if work_items is not None else None,
-        int(work_items.shape[0]) if work_items is not None else 0,
+        max_blocks,
+        plan.data_ptr(),
+        int(plan.shape[0]),
         workspace.data_ptr(),
-        tickets.data_ptr(),
-        SEPARATE_REDUCE if separate_reduce else 0,
         _stream(pool.device),
     )
     _check(lib, "pc_paged_decode_attn", status)

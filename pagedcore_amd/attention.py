@@ -38,7 +38,6 @@ def _launch(
     allocator: KVAllocator,
     request_ids: Sequence[RequestId],
     layer_index: int,
-    partition_blocks: Optional[int],
 ) -> Tensor:
     tables, lengths = allocator.gather_block_tables(request_ids, layer_index=layer_index)
     pool = allocator.pool
@@ -51,11 +50,8 @@ def _launch(
     if not q.is_contiguous():
         q = q.contiguous()
     out = torch.empty((batch, Q_HEADS, 1, HEAD_DIM), dtype=torch.float16, device=query.device)
-    parts = partition_blocks if partition_blocks is not None else _hip.default_partition_blocks()
-    items = allocator.decode_work_items(request_ids, layer_index=layer_index, partition_blocks=parts)
-    _hip.paged_decode_attention(
-        out, q, pool, layer_index, tables, lengths, partition_blocks=parts, work_items=items
-    )
+    plan = allocator.decode_plan(request_ids, layer_index=layer_index)
+    _hip.paged_decode_attention(out, q, pool, layer_index, tables, lengths, plan=plan)
     return out
 
 
@@ -74,7 +70,7 @@ def paged_attention(
     _check_layer(layer_index)
     if eager_rounding:
         raise ValueError("eager_rounding replays HF fp16 rounding and is not part of the GPU path")
-    return _launch(query, allocator, (request_id,), layer_index, None)
+    return _launch(query, allocator, (request_id,), layer_index)
 
 
 @torch.inference_mode()
@@ -84,7 +80,6 @@ def paged_attention_batch(
     request_ids: Sequence[RequestId],
     *,
     layer_index: int,
-    partition_blocks: Optional[int] = None,
 ) -> Tensor:
     """Decode attention for FP16 [B, 32, 1, 64] queries; row b attends request_ids[b]."""
     batch = len(request_ids)
@@ -93,4 +88,4 @@ def paged_attention_batch(
     if len(set(request_ids)) != batch:
         raise ValueError("attention requires distinct request IDs")
     _check_layer(layer_index)
-    return _launch(query, allocator, tuple(request_ids), layer_index, partition_blocks)
+    return _launch(query, allocator, tuple(request_ids), layer_index)

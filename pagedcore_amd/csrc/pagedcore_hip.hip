@@ -1,6 +1,7 @@
-// Paged KV-cache hot path for MI355X (gfx950): KV append, paged decode attention with
-// split-K partitions, and the partition reduce. Exposed through the C ABI declared in
-// include/pagedcore_hip.h. No allocation happens here; every buffer comes from the caller.
+// Paged KV-cache hot path for MI355X (gfx950): KV append, paged decode attention over split-K
+// work items, and the merge of the items' partials. Exposed through the C ABI declared in
+// include/pagedcore_hip.h. No device memory is allocated here; every buffer comes from the
+// caller.
 //
 // Pool layout (fixed by the reference allocator, src/pagedcore/kv_cache.py:39-43):
 //   fp16 [22 layers][2 kinds][num_blocks][16 slots][4 kv heads][64 dims]
@@ -10,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <vector>
 
 #include <math.h>
 #include <stdarg.h>
@@ -20,7 +22,7 @@
 
 namespace {
 
-constexpr int kAbiVersion = 6;
+constexpr int kAbiVersion = 7;
 constexpr int kLayers = 22;
 constexpr int kSlots = 16;
 constexpr int kKVHeads = 4;
@@ -141,31 +143,35 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_word_kernel(
 // ---------------------------------------------------------------------------------------
 // Paged decode attention.
 //
-// Split-K over work items: item i of sequence b covers blocks [W i, W i + W) of its table
-// (W = partition_blocks, 1/2/4/8) for all 4 kv heads. One workgroup of W waves per item;
-// wave w owns block W i + w and issues every load of that block at once:
-//   * K, 8 KiB: per kv head h two 16 B loads per lane, lane (c = lane % 16, g = lane / 16)
-//     taking K[slot c][h][8g .. 8g + 7] and [32 + 8g ..] -- already the A operand of
-//     v_mfma_f32_16x16x32_f16;
-//   * V, 8 KiB: eight 16 B loads per lane, each instruction one contiguous KiB (whole 128 B
-//     lines), staged through LDS rows of 512 B + 32 B pad.
-// No wave ever waits for a second round of loads, so the whole grid's requests are in the
-// memory queues at once and the kernel drains HBM at its streaming rate.
+// Work split. A work item is 9 consecutive blocks of one sequence (the last item of a
+// sequence may hold fewer) and runs as one workgroup of 12 waves: wave w serves kv head
+// h = w % 4 for sub-chunk s = w / 4, i.e. blocks [9 item + 3 s, 9 item + 3 s + 3). Every
+// load of a wave is issued before its first block is processed:
+//   * Q of the head's 8 query heads (1 KiB, from L2 after the first item of the sequence);
+//   * K, per block 16 rows x 128 B: lane (c = lane % 16, g = lane / 16) loads row c, dims
+//     8g..8g+7 and 32+8g..39+8g -- the A operand of v_mfma_f32_16x16x32_f16 -- into VGPRs;
+//   * V, per block 16 rows x 128 B, straight into the wave's LDS area by LDS DMA
+//     (global_load_lds_dwordx4), each 32 B dim group of row r stored at group position
+//     u ^ sel(r) so that the transposing reads below are free of bank conflicts.
+// A CU holds two such workgroups (72 KiB of LDS and 77 VGPRs each), so a 64-sequence decode
+// batch is in flight in one round and HBM drains at its streaming rate.
 //
-// Per kv head (all in registers, one block so no online rescaling):
-//   * S^T[16 tokens][16] = K . Q^T on the matrix core (columns 8..15 repeat q heads 0..7);
-//     lane (c, g) receives the raw dots of q head 8h + c % 8 for tokens 4g .. 4g + 3;
-//   * masked tokens (past the context) become -inf and their V rows are zeroed in LDS,
-//     so poisoned tail slots never reach a product (0 x NaN would);
-//   * p = 2^((dot - max) log2(e) / 8): the 1/8 scale is applied to the exact difference;
-//   * O[16][16 dims] += P . V with v_mfma_f32_16x16x16f16: rows 0..7 carry the fp16
-//     rounding of p, rows 8..15 the remainder scaled by 2^18, so the product keeps fp32
-//     accuracy; V reaches the B layout through transposing LDS reads (ds_read_b64_tr_b16).
-// The W waves then meet in LDS: each thread folds D = 32 / W outputs of one q head over
-// the waves (max / rescale / sum). A sequence that fits one item writes fp16 output;
-// otherwise the item's (max, sum, unnormalized output) goes to the workspace and the
-// sequence's items are merged by paged_decode_merge_kernel, or -- flags 0 -- by the last
-// workgroup of the sequence to finish (atomic ticket).
+// Per block (online softmax, fp32):
+//   * S^T[16 tokens][16] = K . Q^T on the matrix core (columns 8..15 repeat q heads 0..7):
+//     lane (c, g) holds the raw dots of q head c % 8 for tokens 4g..4g+3;
+//   * tokens past the context become -inf and their V rows are zeroed in the B operand, so
+//     poisoned tail slots never reach a product (0 x NaN would);
+//   * the running max is raised only when a score exceeds it by 2^8 in probability (a
+//     ballot over the wave); otherwise p = 2^((dot - max) log2(e) / 8) needs no cross-lane
+//     reduction;
+//   * O[16][64] += P . V with v_mfma_f32_16x16x16f16: rows 0..7 carry the fp16 rounding of
+//     p, rows 8..15 the remainder scaled by 2^18, so the product keeps fp32 accuracy over
+//     the range p in [2^-32, 2^8]; V reaches the B layout through ds_read_b64_tr_b16.
+// The three sub-chunk waves of a head then merge through LDS: each leaves (max, sum,
+// unnormalized O) in its area and takes an LDS ticket; the last one folds them in
+// sub-chunk order. A sequence that is one item writes its fp16 output directly; otherwise
+// the item's partial goes to the workspace and paged_decode_merge_kernel folds the items of
+// each (sequence, kv head) in item order.
 // ---------------------------------------------------------------------------------------
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -174,29 +180,45 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kDefaultPartitionBlocks = 8;
-constexpr int kVPitch = 544;                   // bytes per staged V row: 512 B of data + 32 B pad
-constexpr int kWaveLds = kSlots * kVPitch;     // 8704 B of LDS per wave
-constexpr int kItemOutputs = kQHeads * kHeadDim;  // 2048 fp32 outputs per item
-constexpr int kMergeThreads = 256;             // separate merge: one workgroup per (sequence, 8 q heads)
-// Plan record: {sequence, item, context length, closer flag, block ids of the item's W
-// blocks (0 past the sequence's last block)}, padded to a multiple of 4 int32.
-constexpr int kPlanHeader = 4;
-// Ticket polls a closer makes before giving up on its siblings (each a round trip of about
-// a microsecond plus a short sleep): ends the wait well under a second in any case.
-constexpr int kCloserPolls = 1 << 16;
-constexpr int plan_fields(int w) { return kPlanHeader + (w + 3) / 4 * 4; }
+constexpr int kSubBlocks = 3;                              // blocks per wave
+constexpr int kSubs = 3;                                   // sub-chunk waves per kv head
+constexpr int kItemBlocks = kSubBlocks * kSubs;            // 9 blocks per work item
+constexpr int kItemWaves = kKVHeads * kSubs;               // 12 waves per workgroup
+constexpr int kItemThreads = 64 * kItemWaves;
+constexpr int kHeadBlockBytes = kSlots * kHeadDim * 2;     // one kv head of one block: 2 KiB
+constexpr int kAreaBytes = kSubBlocks * kHeadBlockBytes;   // LDS per wave: 6 KiB
+constexpr int kPlanInts = 16;                              // {seq, item, len, items, 9 ids, 3 x 0}
+constexpr int kPlanBins = 8;                               // XCDs of an MI355X
+constexpr int kPartFloats = kGroup * kHeadDim + 2 * kGroup;  // item partial: O [8][64], (m, l) x 8
+constexpr int kMergeThreads = 256;
+constexpr int kMergeItems = 16;                            // items per merge round trip
 // log2(e) / sqrt(64): turns a raw q.k difference into a base-2 exponent.
 constexpr float kScoreToLog2 = 0.18033688011112042f;
 // Scale of the low (remainder) part of p in the PV product (2^18).
 constexpr float kLowScale = 262144.0f;
-static_assert(kWaveLds >= (kItemOutputs + 2 * kQHeads) * 4, "a wave's LDS also holds its partial");
+// Headroom (log2 of p) before the running max is raised.
+constexpr float kLazyLog2 = 8.0f;
+
+struct AttnArgs {
+  _Float16* out;
+  const _Float16* query;
+  const _Float16* pool;
+  int64_t num_blocks;
+  const int32_t* plan;
+  const int32_t* context_lens;
+  float* partials;  // [batch][4 kv heads][max_items][kPartFloats]
+  int layer, batch, max_blocks, max_items;
+};
+
+__device__ __forceinline__ int items_of(int len, int max_blocks) {
+  return len > 0 ? (min((len + kSlots - 1) / kSlots, max_blocks) + kItemBlocks - 1) / kItemBlocks : 0;
+}
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Max / sum over the 4 lanes l, l^16, l^32, l^48 (one q head's 4 token groups); every
-// lane gets the result.
+// Max / sum over the 4 lanes l, l^16, l^32, l^48 (one q head's 4 token groups).
 __device__ __forceinline__ float max_over_groups(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -211,484 +233,412 @@ __device__ __forceinline__ float sum_over_groups(float x) {
   return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
-// Reduce-scatter of a PV tile pair over the wave halves: lanes < 32 get
-// x[l] + x[l + 32] / 2^18, lanes >= 32 get y[l - 32] + y[l] / 2^18 (the high rows of a
-// 16x16 tile sit in lanes 0..31, its scaled low rows in lanes 32..63).
+// Reduce-scatter of a PV tile pair over the wave halves: lanes < 32 get x[l] + x[l + 32] / 2^18,
+// lanes >= 32 get y[l - 32] + y[l] / 2^18 (high rows of a tile in lanes 0..31, scaled low rows
+// in lanes 32..63).
 __device__ __forceinline__ float fold_low_rows(float x, float y) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
   return fmaf(__uint_as_float(r[1]), 1.0f / kLowScale, __uint_as_float(r[0]));
 }
 
-// LDS ordering inside one wave: the compiler keeps LDS accesses on their side of this
-// point and the wave's LDS operations complete in issue order.
+// LDS ordering inside one wave.
 __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-struct AttnArgs {
-  _Float16* out;
-  const _Float16* query;
-  const _Float16* pool;
-  int64_t num_blocks;
-  const int32_t* block_tables;
-  const int32_t* context_lens;
-  float* ws_out;     // [batch][max_items][32 q heads][64] unnormalized item outputs
-  float* ws_ml;      // [batch][max_items][32 q heads][2] (max of raw dots, sum of p)
-  int32_t* tickets;  // [batch] merge tickets, zero between calls
-  const int32_t* work_items;  // (sequence, item) pairs, or null: every (sequence, item slot)
-  int layer, max_blocks, batch, max_items, fused_merge;
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+__device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(char* p) {
+  return (__attribute__((address_space(3))) void*)p;
+}
+
+// Dim group u (dims 16u..16u+15) of staged V row r sits at group position u ^ row_sel(r):
+// the four rows one transposing read touches per 16 lanes land in four different 32 B bank
+// groups, and so do the even and the odd rows of any eight.
+__device__ __forceinline__ int row_sel(int r) { return (r + (r >> 2)) & 3; }
+
+// The four transposing reads of one staged block (B operands of the four 16-dim tiles). The
+// loads are written out so that the compiler does not treat them as waiting on the LDS DMA
+// (it would wait for every outstanding load); the wave has waited for this block's DMA.
+template <int kOff>
+__device__ __forceinline__ void read_v_tiles(uint32_t base, uint32_t sel, short4_t& r0, short4_t& r1, short4_t& r2,
+                                             short4_t& r3) {
+  const uint32_t a0 = base + 32 * (0 ^ sel), a1 = base + 32 * (1 ^ sel), a2 = base + 32 * (2 ^ sel),
+                 a3 = base + 32 * (3 ^ sel);
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %4 offset:%8\n\t"
+      "ds_read_b64_tr_b16 %1, %5 offset:%8\n\t"
+      "ds_read_b64_tr_b16 %2, %6 offset:%8\n\t"
+      "ds_read_b64_tr_b16 %3, %7 offset:%8\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "i"(kOff)
+      : "memory");
+}
+
+// 16 B at p and p + 64 B, issued without compiler tracking; wait_loads<N>() on the same
+// registers (N = loads issued after them) makes them available.
+__device__ __forceinline__ void load_pair(half8_t& x, half8_t& y, const _Float16* p) {
+  asm volatile("global_load_dwordx4 %0, %2, off\n\tglobal_load_dwordx4 %1, %2, off offset:64"
+               : "=&v"(x), "=&v"(y)
+               : "v"(p)
+               : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_loads(half8_t& x, half8_t& y) {
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(x), "+v"(y) : "i"(N) : "memory");
+}
+
+// Every load of the wave has returned. The K registers are named so that none of them is
+// reused while a load of an unused block slot could still land in it.
+__device__ __forceinline__ void wait_all_loads(half8_t (&k0)[kSubBlocks], half8_t (&k1)[kSubBlocks]) {
+  asm volatile("s_waitcnt vmcnt(0)"
+               : "+v"(k0[0]), "+v"(k1[0]), "+v"(k0[1]), "+v"(k1[1]), "+v"(k0[2]), "+v"(k1[2])
+               :
+               : "memory");
+}
+
+__device__ __forceinline__ float lane_value(float x, int k) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
+}
+
+// Online-softmax state of the 4 q heads a lane holds in the PV layout (q head 4(g&1) + r,
+// dims 16(2k + g/2) + c), with the fold of one more partial. Explicit fmaf: every fold
+// rounds the same way wherever it runs.
+struct Fold {
+  float M[4], L[4], O[2][4];
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      M[r] = -INFINITY;
+      L[r] = 0.f;
+      O[0][r] = 0.f;
+      O[1][r] = 0.f;
+    }
+  }
+  __device__ __forceinline__ void add(const float (&m)[4], const float (&l)[4], const float (&x)[2][4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float mn = fmaxf(M[r], m[r]);
+      const float so = exp2_fast((M[r] - mn) * kScoreToLog2);
+      const float sn = exp2_fast((m[r] - mn) * kScoreToLog2);
+      L[r] = fmaf(l[r], sn, L[r] * so);
+      O[0][r] = fmaf(x[0][r], sn, O[0][r] * so);
+      O[1][r] = fmaf(x[1][r], sn, O[1][r] * so);
+      M[r] = mn;
+    }
+  }
 };
 
-// Items of a sequence (0 for an empty one); nblk = its block count, clamped to the table.
-__device__ __forceinline__ int items_of(int len, int max_blocks, int w, int& nblk) {
-  nblk = len > 0 ? min((len - 1) / kSlots + 1, max_blocks) : 0;
-  return (nblk + w - 1) / w;
-}
-
-// Agent-coherent accesses (global_store / global_load ... sc1): partials published by a
-// workgroup on one XCD are visible to a workgroup on any XCD without a cache writeback or
-// invalidate. The plain variants serve the separate merge kernel, which runs after the
-// item kernel has completed.
-template <bool kCoherent>
-__device__ __forceinline__ void store_f2(float* p, float x, float y) {
-  if constexpr (kCoherent) {
-    const uint64_t bits = (static_cast<uint64_t>(__float_as_uint(y)) << 32) | __float_as_uint(x);
-    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
-    *reinterpret_cast<float2_t*>(p) = float2_t{x, y};
+// A sub-chunk partial in its wave's LDS area: lane L's 8 O values at [L][8] floats (value
+// (k, r) at 4k + r), then (m, l) of q head j at byte 2048 + 8j.
+__device__ __forceinline__ void put_sub(char* area, int lane, int g, const float (&x)[2][4], const float (&m)[4],
+                                        const float (&l)[4]) {
+  *reinterpret_cast<float4_t*>(area + lane * 32) = float4_t{x[0][0], x[0][1], x[0][2], x[0][3]};
+  *reinterpret_cast<float4_t*>(area + lane * 32 + 16) = float4_t{x[1][0], x[1][1], x[1][2], x[1][3]};
+  if (lane == 0 || lane == 16) {
+    *reinterpret_cast<float4_t*>(area + 2048 + (g & 1) * 32) = float4_t{m[0], l[0], m[1], l[1]};
+    *reinterpret_cast<float4_t*>(area + 2048 + (g & 1) * 32 + 16) = float4_t{m[2], l[2], m[3], l[3]};
   }
 }
 
-template <bool kCoherent>
-__device__ __forceinline__ float2_t load_f2(const float* p) {
-  if constexpr (kCoherent) {
-    const uint64_t x = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-    return float2_t{__uint_as_float(static_cast<uint32_t>(x)), __uint_as_float(static_cast<uint32_t>(x >> 32))};
-  } else {
-    return *reinterpret_cast<const float2_t*>(p);
+__device__ __forceinline__ void get_sub(const char* area, int lane, int g, float (&x)[2][4], float (&m)[4], float (&l)[4]) {
+  const float4_t x0 = *reinterpret_cast<const float4_t*>(area + lane * 32);
+  const float4_t x1 = *reinterpret_cast<const float4_t*>(area + lane * 32 + 16);
+  const float4_t y0 = *reinterpret_cast<const float4_t*>(area + 2048 + (g & 1) * 32);
+  const float4_t y1 = *reinterpret_cast<const float4_t*>(area + 2048 + (g & 1) * 32 + 16);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    x[0][r] = x0[r];
+    x[1][r] = x1[r];
   }
+  m[0] = y0[0]; l[0] = y0[1]; m[1] = y0[2]; l[1] = y0[3];
+  m[2] = y1[0]; l[2] = y1[1]; m[3] = y1[2]; l[3] = y1[3];
 }
 
-// Items whose partials one merge round trip loads, for D outputs per thread.
-constexpr int merge_batch(int d) { return d <= 2 ? 32 : (d <= 4 ? 16 : (d <= 8 ? 8 : 4)); }
-
-// Folds items [i_begin, nitems) of sequence b into the running state (m, l, o) for dims
-// [o0, o0 + D) of q head `qhead` (D even) with the online-softmax rule; the loads of
-// merge_batch(D) items are issued before any of them is used. Returns the normalized
-// outputs in `res`.
-template <bool kCoherent, int D>
-__device__ __forceinline__ void merge_items_from(const AttnArgs& a, int b, int i_begin, int nitems, int qhead, int o0,
-                                                 float m, float l, float (&o)[D], float (&res)[D]) {
-  constexpr int kBatch = merge_batch(D);
-  const int64_t first = static_cast<int64_t>(b) * a.max_items;
-#pragma unroll 1
-  for (int i0 = i_begin; i0 < nitems; i0 += kBatch) {
-    float2_t ml[kBatch];
-    float2_t x[kBatch][D / 2];
+// PV-layout values to natural order [8 q heads][64] through `area`: the fp16 output rows
+// (scaled by inv[r]) or the fp32 item partial; each lane then stores 16 or 32 contiguous bytes.
+template <bool kHalf>
+__device__ __forceinline__ void store_natural(void* dst, char* area, int lane, const float (&x)[2][4], const float (&inv)[4]) {
+  const int c = lane & 15, g = lane >> 4;
+  wave_lds_fence();
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int64_t p = first + min(i0 + j, nitems - 1);  // clamped: always in bounds
-      ml[j] = load_f2<kCoherent>(a.ws_ml + (p * kQHeads + qhead) * 2);
-      const float* xp = a.ws_out + p * kItemOutputs + qhead * kHeadDim + o0;
+  for (int k = 0; k < 2; ++k)
 #pragma unroll
-      for (int i = 0; i < D / 2; ++i) x[j][i] = load_f2<kCoherent>(xp + 2 * i);
-    }
-    // Branch-free fold (a branch would let the compiler sink each load to its use): a
-    // clamped duplicate gets weight 0; m is finite from the first item on, so m_new is too.
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const float mp = (i0 + j < nitems) ? ml[j][0] : -INFINITY;
-      const float m_new = fmaxf(m, mp);
-      const float s_old = exp2_fast((m - m_new) * kScoreToLog2);  // 0 while m = -inf
-      const float s_new = exp2_fast((mp - m_new) * kScoreToLog2);  // 0 for a duplicate
-      // Explicit fmaf: every instantiation (and so both merge modes) rounds identically.
-      l = fmaf(ml[j][1], s_new, l * s_old);
-#pragma unroll
-      for (int i = 0; i < D / 2; ++i) {
-        o[2 * i] = fmaf(x[j][i][0], s_new, o[2 * i] * s_old);
-        o[2 * i + 1] = fmaf(x[j][i][1], s_new, o[2 * i + 1] * s_old);
+    for (int r = 0; r < 4; ++r) {
+      const int idx = (4 * (g & 1) + r) * kHeadDim + 16 * (2 * k + (g >> 1)) + c;
+      if constexpr (kHalf) {
+        reinterpret_cast<_Float16*>(area)[idx] = static_cast<_Float16>(x[k][r] * inv[r]);
+      } else {
+        reinterpret_cast<float*>(area)[idx] = x[k][r];
       }
-      m = m_new;
     }
-  }
-  const float inv = 1.0f / l;
-#pragma unroll
-  for (int i = 0; i < D; ++i) res[i] = o[i] * inv;
-}
-
-template <bool kCoherent, int D>
-__device__ __forceinline__ void merge_items(const AttnArgs& a, int b, int nitems, int qhead, int o0, float (&res)[D]) {
-  float o[D];
-#pragma unroll
-  for (int i = 0; i < D; ++i) o[i] = 0.f;
-  merge_items_from<kCoherent, D>(a, b, 0, nitems, qhead, o0, -INFINITY, 0.f, o, res);
-}
-
-// The closer's fold: items [0, nitems) of sequence b in item order with the same
-// arithmetic as merge_items, item `own` taken from registers (m_own, l_own, x_own) and the
-// others through agent-coherent loads. Unused batch slots and the own item's (never
-// written) workspace entries are selected out, never multiplied, so the result is
-// bit-identical to the separate merge.
-template <int D>
-__device__ __forceinline__ void merge_with_own(const AttnArgs& a, int b, int nitems, int own, int qhead, int o0,
-                                               float m_own, float l_own, const float (&x_own)[D], float (&res)[D]) {
-  constexpr int kBatch = merge_batch(D);
-  float m = -INFINITY, l = 0.f, o[D];
-#pragma unroll
-  for (int i = 0; i < D; ++i) o[i] = 0.f;
-  const int64_t first = static_cast<int64_t>(b) * a.max_items;
-#pragma unroll 1
-  for (int i0 = 0; i0 < nitems; i0 += kBatch) {
-    float2_t ml[kBatch];
-    float2_t x[kBatch][D / 2];
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int64_t p = first + min(i0 + j, nitems - 1);  // clamped: always in bounds
-      ml[j] = load_f2<true>(a.ws_ml + (p * kQHeads + qhead) * 2);
-      const float* xp = a.ws_out + p * kItemOutputs + qhead * kHeadDim + o0;
-#pragma unroll
-      for (int i = 0; i < D / 2; ++i) x[j][i] = load_f2<true>(xp + 2 * i);
-    }
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int idx = i0 + j;
-      const bool used = idx < nitems;
-      const bool mine = idx == own;
-      const float mp = !used ? -INFINITY : (mine ? m_own : ml[j][0]);
-      const float lp = !used ? 0.f : (mine ? l_own : ml[j][1]);
-      const float m_new = fmaxf(m, mp);
-      const float s_old = exp2_fast((m - m_new) * kScoreToLog2);
-      const float s_new = exp2_fast((mp - m_new) * kScoreToLog2);
-      l = fmaf(lp, s_new, l * s_old);
-#pragma unroll
-      for (int i = 0; i < D / 2; ++i) {
-        const float x0 = !used ? 0.f : (mine ? x_own[2 * i] : x[j][i][0]);
-        const float x1 = !used ? 0.f : (mine ? x_own[2 * i + 1] : x[j][i][1]);
-        o[2 * i] = fmaf(x0, s_new, o[2 * i] * s_old);
-        o[2 * i + 1] = fmaf(x1, s_new, o[2 * i + 1] * s_old);
-      }
-      m = m_new;
-    }
-  }
-  const float inv = 1.0f / l;
-#pragma unroll
-  for (int i = 0; i < D; ++i) res[i] = o[i] * inv;
-}
-
-template <int D>
-__device__ __forceinline__ void store_out(_Float16* dst, const float (&v)[D]) {
-#pragma unroll
-  for (int i = 0; i < D; i += 2) {
-    *reinterpret_cast<half2_t*>(dst + i) = half2_t{static_cast<_Float16>(v[i]), static_cast<_Float16>(v[i + 1])};
+  wave_lds_fence();
+  char* d = static_cast<char*>(dst);
+  if constexpr (kHalf) {
+    *reinterpret_cast<uint4*>(d + lane * 16) = *reinterpret_cast<const uint4*>(area + lane * 16);
+  } else {
+    *reinterpret_cast<uint4*>(d + lane * 32) = *reinterpret_cast<const uint4*>(area + lane * 32);
+    *reinterpret_cast<uint4*>(d + lane * 32 + 16) = *reinterpret_cast<const uint4*>(area + lane * 32 + 16);
   }
 }
 
-template <int W, bool kPlanned>
-__global__ __launch_bounds__(64 * W) void paged_decode_item_kernel(AttnArgs a) {
-  constexpr int D = kItemOutputs / (64 * W);  // outputs per thread in the workgroup merge
-  __shared__ __attribute__((aligned(16))) char lds[W * kWaveLds];
-  __shared__ int32_t ticket_slot;
-
-  // Wave index as a scalar, so every per-wave address below is scalar arithmetic and the
-  // block-id loads are scalar loads.
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+__global__ __launch_bounds__(kItemThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void paged_decode_item_kernel(
+    AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) char lds[kItemWaves * kAreaBytes];
+  __shared__ int32_t sub_tickets[kKVHeads];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = w & 3;
+  const int s = w >> 2;
   const int lane = threadIdx.x & 63;
   const int c = lane & 15;
   const int g = lane >> 4;
 
-  int b, item, len;
-  int32_t id;
-  bool closer;  // merges the sequence's items (fused merge)
-  const int blk_in_item = wave;
-  if constexpr (kPlanned) {
-    // Planned grid: one workgroup per item that exists. The record header and this
-    // wave's block id are requested together, before any branch, so the KV loads leave
-    // after a single round trip.
-    const int32_t* rec = a.work_items + static_cast<int64_t>(blockIdx.x) * plan_fields(W);
-    const int4 hdr = *reinterpret_cast<const int4*>(rec);
-    id = rec[kPlanHeader + blk_in_item];
-    // A record outside the batch or the workspace is skipped at the item check below; it
-    // is clamped, not branched on, here so that no load waits behind the check.
-    const bool in_range = static_cast<uint32_t>(hdr.x) < static_cast<uint32_t>(a.batch) &&
-                          static_cast<uint32_t>(hdr.y) < static_cast<uint32_t>(a.max_items);
-    b = in_range ? hdr.x : 0;
-    item = in_range ? hdr.y : a.max_items;
-    len = hdr.z;
-    closer = hdr.w != 0;
-    // The block id is consumed here so that its load leaves with the header's instead
-    // of after the item check below.
-    asm volatile("" ::"s"(id));
-  } else {
-    // Full grid: item slots past a sequence's length exit below; the length and this
-    // wave's block id come from the device tables in one round trip.
-    b = blockIdx.x % a.batch;
-    item = blockIdx.x / a.batch;
-    id = a.block_tables[static_cast<int64_t>(b) * a.max_blocks + min(item * W + blk_in_item, a.max_blocks - 1)];
-    len = a.context_lens[b];
-  }
-  const int blk = item * W + blk_in_item;
-  // B operand = Q^T per kv head h: column c is q head 8h + c % 8.
-  const _Float16* qrow = a.query + (static_cast<int64_t>(b) * kQHeads + (c & 7)) * kHeadDim + 8 * g;
-  half8_t qa[kKVHeads], qb[kKVHeads];
+  // The whole plan record in one scalar load; this wave's block ids are selected from it.
+  const int32_t* rec = a.plan + static_cast<int64_t>(blockIdx.x) * kPlanInts;
+  int32_t r[kPlanInts];
 #pragma unroll
-  for (int h = 0; h < kKVHeads; ++h) {
-    qa[h] = *reinterpret_cast<const half8_t*>(qrow + h * kGroup * kHeadDim);
-    qb[h] = *reinterpret_cast<const half8_t*>(qrow + h * kGroup * kHeadDim + 32);
-  }
-  int nblk;
-  const int nitems = items_of(len, a.max_blocks, W, nblk);
-  if (item >= nitems) return;  // uniform over the workgroup
-  if constexpr (!kPlanned) closer = item == nitems - 1;  // the sequence's highest workgroup index
-  const bool active = blk < nblk;  // uniform over the wave; wave 0 is always active
+  for (int i = 0; i < kPlanInts; ++i) r[i] = rec[i];
+  const int b = r[0];
+  const int item = r[1];
+  const int len = r[2];
+  // Padding records (b < 0) and records that do not fit the call's shapes do nothing: the
+  // whole workgroup leaves before the barrier.
+  if (b < 0 || b >= a.batch || item < 0 || item >= items_of(len, a.max_blocks) || item >= a.max_items) return;
+  const int nitems = items_of(len, a.max_blocks);
+  int32_t ids[kSubBlocks];
+#pragma unroll
+  for (int t = 0; t < kSubBlocks; ++t) ids[t] = s == 0 ? r[4 + t] : (s == 1 ? r[4 + kSubBlocks + t] : r[4 + 2 * kSubBlocks + t]);
+  const int nblk = min((len + kSlots - 1) / kSlots, a.max_blocks);
+  const int count = min(kItemBlocks, nblk - item * kItemBlocks);  // blocks of this item, >= 1
+  const int nsub = (count + kSubBlocks - 1) / kSubBlocks;
+  const int first = item * kItemBlocks + s * kSubBlocks;          // first block of this wave
+  const int mine = min(kSubBlocks, count - s * kSubBlocks);       // its blocks (if s < nsub)
+  char* area = lds + (h * kSubs + s) * kAreaBytes;
 
-  char* vl = lds + wave * kWaveLds;
-  float* part = reinterpret_cast<float*>(vl);  // after PV: [32 q heads][64] outputs, then (m, l) pairs
-  if (active) {
-    uint32_t phys = static_cast<uint32_t>(id);
-    const bool bad = phys >= static_cast<uint64_t>(a.num_blocks);  // negative ids wrap to huge values
-    if (bad) phys = 0;  // never dereferenced out of the pool
+  // The LDS tickets are zeroed before any wave can take one. The waves of a workgroup start
+  // together, and the record is in registers first, so no load waits behind this barrier.
+  if (w == 0 && lane < kKVHeads) sub_tickets[lane] = 0;
+  asm volatile("" ::"s"(item), "s"(len), "s"(ids[0]), "s"(ids[1]), "s"(ids[2]));
+  __syncthreads();
+  if (s >= nsub) return;
+
+  half8_t qa, qb, k0[kSubBlocks], k1[kSubBlocks];
+  bool bad = false;
+  {
     const int64_t kind_elems = a.num_blocks * kBlockElems;
-    const _Float16* kblk = a.pool + static_cast<int64_t>(a.layer) * 2 * kind_elems + static_cast<int64_t>(phys) * kBlockElems;
-    const char* vblk = reinterpret_cast<const char*>(kblk + kind_elems);
-    half8_t k0[kKVHeads], k1[kKVHeads];
+    const _Float16* qrow = a.query + (static_cast<int64_t>(b) * kQHeads + kGroup * h + (c & 7)) * kHeadDim + 8 * g;
+    load_pair(qa, qb, qrow);
+    const _Float16* lbase = a.pool + static_cast<int64_t>(a.layer) * 2 * kind_elems + h * kHeadDim;
+    // LDS DMA slots: instruction 0 fills rows 0..7, instruction 1 rows 8..15; lane holds the
+    // 16 B chunk stored at position lane % 8 of row lane / 8 (+ 8).
+    const int qs = lane & 7;
+    const int rA = lane >> 3, rB = rA + 8;
+    const int offA = rA * kRowElems + 8 * (2 * ((qs >> 1) ^ row_sel(rA)) + (qs & 1));
+    const int offB = rB * kRowElems + 8 * (2 * ((qs >> 1) ^ row_sel(rB)) + (qs & 1));
 #pragma unroll
-    for (int h = 0; h < kKVHeads; ++h) {
-      k0[h] = *reinterpret_cast<const half8_t*>(kblk + c * kRowElems + h * kHeadDim + 8 * g);
-      k1[h] = *reinterpret_cast<const half8_t*>(kblk + c * kRowElems + h * kHeadDim + 32 + 8 * g);
-    }
-    uint4 vraw[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) vraw[q] = *reinterpret_cast<const uint4*>(vblk + q * 1024 + lane * 16);
-
-    const int valid = len - blk * kSlots;  // >= 1; below 16 only in the sequence's last block
-    // V rows to LDS; in the sequence's last block the rows of masked slots are zeroed.
-    char* vdst = vl + (lane >> 5) * kVPitch + (lane & 31) * 16;
-    if (valid >= kSlots) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) *reinterpret_cast<uint4*>(vdst + 2 * q * kVPitch) = vraw[q];
-    } else {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int slot = 2 * q + (lane >> 5);
-        *reinterpret_cast<uint4*>(vdst + 2 * q * kVPitch) = slot < valid ? vraw[q] : uint4{0, 0, 0, 0};
+    for (int t = 0; t < kSubBlocks; ++t) {
+      uint32_t id = static_cast<uint32_t>(ids[t]);
+      if (id >= static_cast<uint64_t>(a.num_blocks)) {  // negative ids wrap to huge values
+        if (t < mine) bad = true;
+        id = 0;  // never dereferenced out of the pool
       }
+      const _Float16* kb = lbase + static_cast<int64_t>(id) * kBlockElems;
+      load_pair(k0[t], k1[t], kb + c * kRowElems + 8 * g);
+      const _Float16* vb = kb + kind_elems;
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + offA), lds_ptr(area + t * kHeadBlockBytes), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + offB), lds_ptr(area + t * kHeadBlockBytes + 1024), 16, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);  // keep the issue order the waits below count on
     }
+  }
+
+  // Transposing reads: lane (c, g) supplies row 4g + c/4, 8 B piece c % 4 of a dim group.
+  const int rr = 4 * g + (c >> 2);
+  const uint32_t tbase = lds_offset(area) + rr * 128 + 8 * (c & 3);
+  const uint32_t tsel = row_sel(rr);
+  float m = 0.f, mc = 0.f, lsum = 0.f;
+  float4_t acc[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) acc[nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+#define PC_PROCESS_BLOCK(I)                                                                                     \
+  if (I < mine) {                                                                                               \
+    wait_loads<4 * (kSubBlocks - 1 - I)>(k0[I], k1[I]);                                                          \
+    if (I == 0) wait_loads<4 * (kSubBlocks - 1)>(qa, qb);                                                       \
+    float4_t sv = {0.f, 0.f, 0.f, 0.f};                                                                          \
+    sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0[I], qa, sv, 0, 0, 0);                                          \
+    sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1[I], qb, sv, 0, 0, 0);                                          \
+    const int valid = len - (first + I) * kSlots;                                                               \
+    float sc[4] = {sv[0], sv[1], sv[2], sv[3]};                                                                 \
+    if (valid < kSlots) {                                                                                       \
+      _Pragma("unroll") for (int q = 0; q < 4; ++q) sc[q] = 4 * g + q < valid ? sc[q] : -INFINITY;              \
+    }                                                                                                           \
+    const float bm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));                                           \
+    if (I == 0) {                                                                                               \
+      m = max_over_groups(bm); /* finite: token 0 of a wave's first block is valid */                            \
+      mc = m * kScoreToLog2;                                                                                    \
+    } else if (__builtin_amdgcn_ballot_w64(bm * kScoreToLog2 > mc + kLazyLog2) != 0) {                         \
+      const float mn = fmaxf(m, max_over_groups(bm));                                                           \
+      const float alpha = exp2_fast((m - mn) * kScoreToLog2);                                                   \
+      lsum *= alpha;                                                                                            \
+      float al[4];                                                                                              \
+      _Pragma("unroll") for (int q = 0; q < 4; ++q) al[q] = (g & 1) ? lane_value(alpha, 4 + q) : lane_value(alpha, q); \
+      _Pragma("unroll") for (int nt = 0; nt < 4; ++nt) _Pragma("unroll") for (int q = 0; q < 4; ++q) acc[nt][q] *= al[q]; \
+      m = mn;                                                                                                   \
+      mc = m * kScoreToLog2;                                                                                    \
+    }                                                                                                           \
+    float p[4];                                                                                                 \
+    _Pragma("unroll") for (int q = 0; q < 4; ++q) p[q] = exp2_fast(fmaf(sc[q], kScoreToLog2, -mc));             \
+    lsum += (p[0] + p[1]) + (p[2] + p[3]);                                                                      \
+    /* A operand: row c holds p of q head c % 8 for tokens 4g..4g+3: the fp16 rounding of */                    \
+    /* p for c < 8, the exact remainder scaled by 2^18 for c >= 8 */                                             \
+    half4_t pa;                                                                                                 \
+    _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                                             \
+      const float hi = static_cast<float>(static_cast<_Float16>(p[q]));                                         \
+      pa[q] = static_cast<_Float16>(c < kGroup ? p[q] : (p[q] - hi) * kLowScale);                               \
+    }                                                                                                           \
+    short4_t v0, v1, v2, v3;                                                                                    \
+    read_v_tiles<I * kHeadBlockBytes>(tbase, tsel, v0, v1, v2, v3);                                             \
+    if (valid < kSlots) {                                                                                       \
+      /* lane (c, g) holds V of tokens 4g..4g+3: zero the ones past the context */                             \
+      const int keep = valid - 4 * g;                                                                           \
+      const uint32_t mlo = (keep > 0 ? 0xFFFFu : 0u) | (keep > 1 ? 0xFFFF0000u : 0u);                           \
+      const uint32_t mhi = (keep > 2 ? 0xFFFFu : 0u) | (keep > 3 ? 0xFFFF0000u : 0u);                           \
+      uint2_t u;                                                                                                \
+      u = __builtin_bit_cast(uint2_t, v0); u[0] &= mlo; u[1] &= mhi; v0 = __builtin_bit_cast(short4_t, u);        \
+      u = __builtin_bit_cast(uint2_t, v1); u[0] &= mlo; u[1] &= mhi; v1 = __builtin_bit_cast(short4_t, u);        \
+      u = __builtin_bit_cast(uint2_t, v2); u[0] &= mlo; u[1] &= mhi; v2 = __builtin_bit_cast(short4_t, u);        \
+      u = __builtin_bit_cast(uint2_t, v3); u[0] &= mlo; u[1] &= mhi; v3 = __builtin_bit_cast(short4_t, u);        \
+    }                                                                                                           \
+    acc[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v0), acc[0], 0, 0, 0);        \
+    acc[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v1), acc[1], 0, 0, 0);        \
+    acc[2] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v2), acc[2], 0, 0, 0);        \
+    acc[3] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v3), acc[3], 0, 0, 0);        \
+  }
+
+  PC_PROCESS_BLOCK(0)
+  PC_PROCESS_BLOCK(1)
+  PC_PROCESS_BLOCK(2)
+#undef PC_PROCESS_BLOCK
+  static_assert(kSubBlocks == 3, "three PC_PROCESS_BLOCK expansions");
+  wait_all_loads(k0, k1);
+
+  // This wave's partial in the PV layout: (m, l) per q head and the folded O.
+  const float l = sum_over_groups(lsum);
+  float ox[2][4], om[4], ol[4];
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ox[k][q] = bad ? NAN : fold_low_rows(acc[2 * k][q], acc[2 * k + 1][q]);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    om[q] = (g & 1) ? lane_value(m, 4 + q) : lane_value(m, q);
+    ol[q] = (g & 1) ? lane_value(l, 4 + q) : lane_value(l, q);
+  }
+
+  Fold f;
+  f.init();
+  if (nsub > 1) {
+    // Sub-chunk merge: every wave of kv head h leaves its partial in its own LDS area and
+    // takes a ticket; the last one folds the head's sub-chunks in order.
     wave_lds_fence();
-
-    float o[kKVHeads][2][4];
-    float mh[kKVHeads], lh[kKVHeads];
+    put_sub(area, lane, g, ox, om, ol);
+    int old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(&sub_tickets[h], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != nsub - 1) return;
 #pragma unroll
-    for (int h = 0; h < kKVHeads; ++h) {
-      float4_t s = {0.f, 0.f, 0.f, 0.f};
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0[h], qa[h], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1[h], qb[h], s, 0, 0, 0);
-      float sc[4] = {s[0], s[1], s[2], s[3]};
-      if (valid < kSlots) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sc[r] = 4 * g + r < valid ? sc[r] : -INFINITY;
-      }
-      // Block max of q head c % 8 over all 16 tokens (finite: token 0 is always valid).
-      const float mblk = max_over_groups(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-      float p[4];
-      // exp2(-inf) = 0: masked tokens get no weight.
-#pragma unroll
-      for (int r = 0; r < 4; ++r) p[r] = exp2_fast((sc[r] - mblk) * kScoreToLog2);
-      lh[h] = sum_over_groups((p[0] + p[1]) + (p[2] + p[3]));
-      mh[h] = mblk;
-      // A operand: row c holds p of q head c % 8 for tokens 4g .. 4g + 3: for c < 8 the
-      // fp16 rounding of p, for c >= 8 the remainder scaled by 2^18 (p <= 1 bounds it by
-      // 2^7, and the scale keeps p down to 2^-32 in fp16's normal range).
-      half4_t pa;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float hi = static_cast<float>(static_cast<_Float16>(p[r]));
-        pa[r] = static_cast<_Float16>(c >= kGroup ? (p[r] - hi) * kLowScale : p[r]);
-      }
-      // Lane (c, g) reads row 4g + c/4, dims 16nt + 4(c%4) .. + 3 of head h; the
-      // transposing read hands it V[tokens 4g .. 4g + 3][dim 16nt + c], the B operand.
-      const char* vrow = vl + (4 * g + (c >> 2)) * kVPitch + h * kHeadDim * 2 + 8 * (c & 3);
-      float4_t acc[4];
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const short4_t raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            reinterpret_cast<__attribute__((address_space(3))) short4_t*>(reinterpret_cast<uintptr_t>(vrow + 32 * nt)));
-        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, raw),
-                                                        float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-      }
-      // High rows plus unscaled low rows: lane (c, g) then holds q head 8h + 4(g & 1) + r,
-      // dim 16(2k + g / 2) + c (lanes g < 2 from tile 2k, g >= 2 from tile 2k + 1).
-#pragma unroll
-      for (int k = 0; k < 2; ++k)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[h][k][r] = fold_low_rows(acc[2 * k][r], acc[2 * k + 1][r]);
-    }
-    // The partial overwrites this wave's V rows: every PV read above has been issued.
-    wave_lds_fence();
-#pragma unroll
-    for (int h = 0; h < kKVHeads; ++h)
-#pragma unroll
-      for (int k = 0; k < 2; ++k)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int qh = kGroup * h + 4 * (g & 1) + r;
-          part[qh * kHeadDim + 16 * (2 * k + (g >> 1)) + c] = bad ? NAN : o[h][k][r];
-        }
-    if (lane < kGroup) {
-#pragma unroll
-      for (int h = 0; h < kKVHeads; ++h) {
-        *reinterpret_cast<float2_t*>(part + kItemOutputs + (kGroup * h + lane) * 2) = float2_t{mh[h], lh[h]};
+    for (int s2 = 0; s2 < kSubs; ++s2) {
+      if (s2 < nsub) {
+        float px[2][4], pm[4], pl[4];
+        get_sub(lds + (h * kSubs + s2) * kAreaBytes, lane, g, px, pm, pl);
+        f.add(pm, pl, px);
       }
     }
-  }
-  __syncthreads();
-
-  // Workgroup merge: thread t folds outputs [t D, t D + D) -- q head t D / 64 -- over the
-  // item's active waves.
-  const int t = threadIdx.x;
-  const int qhead = (t * D) / kHeadDim;
-  const int o0 = (t * D) % kHeadDim;
-  const int nact = min(W, nblk - item * W);
-  float m = -INFINITY;
-  for (int w = 0; w < nact; ++w) {
-    m = fmaxf(m, reinterpret_cast<const float*>(lds + w * kWaveLds)[kItemOutputs + qhead * 2]);
-  }
-  float l = 0.f, acc[D];
-#pragma unroll
-  for (int i = 0; i < D; ++i) acc[i] = 0.f;
-  for (int w = 0; w < nact; ++w) {
-    const float* pw = reinterpret_cast<const float*>(lds + w * kWaveLds);
-    const float2_t ml = *reinterpret_cast<const float2_t*>(pw + kItemOutputs + qhead * 2);
-    const float e = exp2_fast((ml[0] - m) * kScoreToLog2);
-    l += ml[1] * e;
-#pragma unroll
-    for (int i = 0; i < D; i += 4) {
-      const float4_t x = *reinterpret_cast<const float4_t*>(pw + qhead * kHeadDim + o0 + i);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i + j] += x[j] * e;
-    }
-  }
-  _Float16* out = a.out + (static_cast<int64_t>(b) * kQHeads + qhead) * kHeadDim + o0;
-  if (nitems == 1) {
-    float res[D];
-    const float inv = 1.0f / l;
-#pragma unroll
-    for (int i = 0; i < D; ++i) res[i] = acc[i] * inv;
-    store_out<D>(out, res);
-    return;
-  }
-  const int64_t pidx = static_cast<int64_t>(b) * a.max_items + item;
-  float* ws_out = a.ws_out + pidx * kItemOutputs + qhead * kHeadDim + o0;
-  float* ws_ml = a.ws_ml + (pidx * kQHeads + qhead) * 2;
-  if (!a.fused_merge) {
-#pragma unroll
-    for (int i = 0; i < D; i += 4) *reinterpret_cast<float4_t*>(ws_out + i) = float4_t{acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
-    if (o0 == 0) store_f2<false>(ws_ml, m, l);
-    return;
-  }
-
-  // Fused merge. Every item but the closer publishes its partial with agent-coherent
-  // stores, waits until they have completed, then bumps the sequence's ticket. The closer
-  // (dispatched after all of them) waits -- a bounded number of polls -- until the ticket
-  // shows every sibling, folds the siblings' partials (agent-coherent loads) and its own
-  // (registers) in item order, writes the output and re-arms the ticket.
-  if (!closer) {
-#pragma unroll
-    for (int i = 0; i < D; i += 2) store_f2<true>(ws_out + i, acc[i], acc[i + 1]);
-    if (o0 == 0) store_f2<true>(ws_ml, m, l);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): every store of this thread has completed
-    __syncthreads();
-    if (t == 0) __hip_atomic_fetch_add(&a.tickets[b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
-  if (t == 0) {
-    int seen = 0;
-    for (int poll = 0; poll < kCloserPolls; ++poll) {
-      seen = __hip_atomic_load(&a.tickets[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (seen >= nitems - 1) break;
-      __builtin_amdgcn_s_sleep(8);
-    }
-    ticket_slot = seen;
-  }
-  __syncthreads();
-  float res[D];
-  if (ticket_slot != nitems - 1) {
-    // The siblings never all arrived within the poll budget: the row becomes NaN rather
-    // than a wait without end.
-#pragma unroll
-    for (int i = 0; i < D; ++i) res[i] = NAN;
   } else {
-    merge_with_own<D>(a, b, nitems, item, qhead, o0, m, l, acc, res);
+    f.add(om, ol, ox);
   }
-  store_out<D>(out, res);
-  if (t == 0) __hip_atomic_store(&a.tickets[b], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  if (nitems == 1) {
+    float inv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) inv[q] = 1.0f / f.L[q];
+    store_natural<true>(a.out + (static_cast<int64_t>(b) * kQHeads + kGroup * h) * kHeadDim, area, lane, f.O, inv);
+    return;
+  }
+  float* part = a.partials + ((static_cast<int64_t>(b) * kKVHeads + h) * a.max_items + item) * kPartFloats;
+  store_natural<false>(part, area, lane, f.O, f.L);
+  if (lane == 0 || lane == 16) {
+    *reinterpret_cast<float4_t*>(part + 512 + (g & 1) * 8) = float4_t{f.M[0], f.L[0], f.M[1], f.L[1]};
+    *reinterpret_cast<float4_t*>(part + 512 + (g & 1) * 8 + 4) = float4_t{f.M[2], f.L[2], f.M[3], f.L[3]};
+  }
 }
 
-// Separate merge of every multi-item sequence: one workgroup per (sequence, group of 8 q
-// heads); thread t folds dims 2(t % 32), +1 of q head 8 (blockIdx % 4) + t / 32, loading
-// up to merge_batch(2) = 32 items' partials per round trip.
-__global__ __launch_bounds__(kMergeThreads) void paged_decode_merge_kernel(AttnArgs a, int w) {
-  const int b = blockIdx.x / kKVHeads;
-  const int qhead = kGroup * (blockIdx.x % kKVHeads) + threadIdx.x / 32;
-  const int o0 = 2 * (threadIdx.x % 32);
-  int nblk;
-  const int nitems = items_of(a.context_lens[b], a.max_blocks, w, nblk);
+// Merge of multi-item sequences: one workgroup per (sequence, kv head); thread t owns dims
+// 2(t % 32), +1 of q head t / 32 and folds the items' partials in item order, the loads of
+// up to kMergeItems items issued at once.
+__global__ __launch_bounds__(kMergeThreads) void paged_decode_merge_kernel(AttnArgs a) {
+  const int grp = blockIdx.x;
+  const int b = grp / kKVHeads, h = grp % kKVHeads;
+  const int t = threadIdx.x;
+  const int qh = t >> 5;
+  const int d = 2 * (t & 31);
+  const int nitems = min(items_of(a.context_lens[b], a.max_blocks), a.max_items);
   if (nitems <= 1) return;
-  float res[2];
-  merge_items<false, 2>(a, b, nitems, qhead, o0, res);
-  store_out<2>(a.out + (static_cast<int64_t>(b) * kQHeads + qhead) * kHeadDim + o0, res);
+  const float* gpart = a.partials + static_cast<int64_t>(grp) * a.max_items * kPartFloats;
+  float M = -INFINITY, L = 0.f, O0 = 0.f, O1 = 0.f;
+#pragma unroll 1
+  for (int i0 = 0; i0 < nitems; i0 += kMergeItems) {
+    float2_t x[kMergeItems], ml[kMergeItems];
+#pragma unroll
+    for (int i = 0; i < kMergeItems; ++i) {
+      const float* p = gpart + static_cast<int64_t>(min(i0 + i, nitems - 1)) * kPartFloats;  // clamped: in bounds
+      x[i] = *reinterpret_cast<const float2_t*>(p + qh * kHeadDim + d);
+      ml[i] = *reinterpret_cast<const float2_t*>(p + 512 + 2 * qh);
+    }
+#pragma unroll
+    for (int i = 0; i < kMergeItems; ++i) {
+      // Branch-free: a clamped duplicate gets weight 0 (m stays finite from the first item).
+      const bool used = i0 + i < nitems;
+      const float mp = used ? ml[i][0] : -INFINITY;
+      const float lp = used ? ml[i][1] : 0.f;
+      const float mn = fmaxf(M, mp);
+      const float so = exp2_fast((M - mn) * kScoreToLog2);
+      const float sn = exp2_fast((mp - mn) * kScoreToLog2);
+      L = fmaf(lp, sn, L * so);
+      O0 = fmaf(used ? x[i][0] : 0.f, sn, O0 * so);
+      O1 = fmaf(used ? x[i][1] : 0.f, sn, O1 * so);
+      M = mn;
+    }
+  }
+  const float inv = 1.0f / L;
+  *reinterpret_cast<half2_t*>(a.out + (static_cast<int64_t>(b) * kQHeads + kGroup * h + qh) * kHeadDim + d) =
+      half2_t{static_cast<_Float16>(O0 * inv), static_cast<_Float16>(O1 * inv)};
 }
 
 // ---------------------------------------------------------------------------------------
-// Host-side validation and workspace layout.
+// Host-side validation, plan and workspace layout.
 // ---------------------------------------------------------------------------------------
 
-int max_items(int32_t max_blocks, int32_t partition_blocks) {
-  return (max_blocks + partition_blocks - 1) / partition_blocks;
-}
+int64_t items_per_sequence(int32_t max_blocks) { return (static_cast<int64_t>(max_blocks) + kItemBlocks - 1) / kItemBlocks; }
 
-bool valid_partition(int32_t p) { return p == 1 || p == 2 || p == 4 || p == 8; }
-
-int check_attn_shape(int32_t batch, int32_t max_blocks, int32_t partition_blocks) {
+int check_attn_shape(int32_t batch, int32_t max_blocks) {
   if (batch < 0 || batch > (1 << 20)) return set_error(PC_ERR_ARGUMENT, "batch %d out of range", batch);
   if (max_blocks < 1 || max_blocks > (1 << 16)) {
     return set_error(PC_ERR_ARGUMENT, "max_blocks %d out of range [1, 65536]", max_blocks);
   }
-  if (!valid_partition(partition_blocks)) {
-    return set_error(PC_ERR_ARGUMENT, "partition_blocks %d is not 1, 2, 4 or 8", partition_blocks);
+  if ((static_cast<int64_t>(batch) + kPlanBins) * items_per_sequence(max_blocks) > INT32_MAX) {
+    return set_error(PC_ERR_ARGUMENT, "attention grid too large");
   }
-  const int64_t grid = static_cast<int64_t>(batch) * max_items(max_blocks, partition_blocks);
-  if (grid > INT32_MAX) return set_error(PC_ERR_ARGUMENT, "attention grid too large");
   return PC_OK;
 }
 
-// Workspace = ws_out floats | ws_ml floats, each region 256 B aligned.
-struct WorkspaceLayout {
-  int64_t out_offset, ml_offset, bytes;
-};
-
-WorkspaceLayout workspace_layout(int32_t batch, int32_t max_blocks, int32_t partition_blocks) {
-  auto round_up = [](int64_t x) { return (x + 255) / 256 * 256; };
-  const int64_t items = static_cast<int64_t>(batch) * max_items(max_blocks, partition_blocks);
-  WorkspaceLayout w;
-  w.out_offset = 0;
-  w.ml_offset = round_up(items * kItemOutputs * 4);
-  w.bytes = w.ml_offset + round_up(items * kQHeads * 2 * 4);
-  return w;
-}
-
 bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
-
-template <int W>
-void launch_items(const AttnArgs& a, unsigned grid, hipStream_t s) {
-  if (a.work_items) {
-    hipLaunchKernelGGL((paged_decode_item_kernel<W, true>), dim3(grid), dim3(64 * W), 0, s, a);
-  } else {
-    hipLaunchKernelGGL((paged_decode_item_kernel<W, false>), dim3(grid), dim3(64 * W), 0, s, a);
-  }
-}
 
 }  // namespace
 
@@ -698,74 +648,67 @@ int pc_abi_version(void) { return kAbiVersion; }
 
 const char* pc_last_error(void) { return g_error; }
 
-int32_t pc_attn_default_partition_blocks(void) { return kDefaultPartitionBlocks; }
+int32_t pc_attn_plan_record_ints(void) { return kPlanInts; }
 
-int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t partition_blocks) {
-  if (check_attn_shape(batch, max_blocks, partition_blocks) != PC_OK) return 0;
-  return workspace_layout(batch, max_blocks, partition_blocks).bytes;
+int64_t pc_attn_plan_capacity(int32_t batch, int32_t max_blocks) {
+  if (check_attn_shape(batch, max_blocks) != PC_OK) return -1;
+  // Greedy binning leaves no bin more than one sequence's items above the average.
+  return (static_cast<int64_t>(batch) + kPlanBins) * items_per_sequence(max_blocks);
 }
 
-int64_t pc_attn_plan_capacity(int32_t batch, int32_t max_blocks, int32_t partition_blocks) {
-  if (check_attn_shape(batch, max_blocks, partition_blocks) != PC_OK) return -1;
-  return static_cast<int64_t>(batch) * max_items(max_blocks, partition_blocks);
+int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks) {
+  if (check_attn_shape(batch, max_blocks) != PC_OK) return 0;
+  return static_cast<int64_t>(batch) * kKVHeads * items_per_sequence(max_blocks) * kPartFloats * 4;
 }
 
-int32_t pc_attn_plan_record_ints(int32_t partition_blocks) {
-  if (!valid_partition(partition_blocks)) {
-    return -set_error(PC_ERR_ARGUMENT, "partition_blocks %d is not 1, 2, 4 or 8", partition_blocks);
-  }
-  return plan_fields(partition_blocks);
-}
-
-int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, int32_t batch,
-                     int32_t max_blocks, int32_t partition_blocks, int32_t* work_items, int64_t capacity) {
-  if (int rc = check_attn_shape(batch, max_blocks, partition_blocks)) return -rc;
-  if (batch > 0 && (!context_lens || !block_tables || !work_items)) {
-    return -set_error(PC_ERR_ARGUMENT, "null pointer");
-  }
-  const int fields = plan_fields(partition_blocks);
-  int64_t total = 0;
-  for (int32_t b = 0; b < batch; ++b) {
+int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, int32_t batch, int32_t max_blocks,
+                     int32_t* plan, int64_t capacity) {
+  if (int rc = check_attn_shape(batch, max_blocks)) return -rc;
+  if (batch > 0 && (!context_lens || !block_tables || !plan)) return -set_error(PC_ERR_ARGUMENT, "null pointer");
+  // Sequences, longest first, go to the bin (XCD) with the fewest items so far; work item k
+  // of bin x becomes record k * kPlanBins + x, and the hardware dispatches workgroup i to XCD
+  // (i + start) % 8, so the items of one sequence share an XCD and its L2. Bins shorter than
+  // the longest are padded with empty records.
+  std::vector<int32_t> order;
+  order.reserve(batch);
+  for (int32_t b = 0; b < batch; ++b)
+    if (context_lens[b] > 0) order.push_back(b);
+  std::stable_sort(order.begin(), order.end(), [&](int32_t x, int32_t y) { return context_lens[x] > context_lens[y]; });
+  std::vector<std::vector<int32_t>> bins(kPlanBins);
+  std::vector<int64_t> load(kPlanBins, 0);
+  for (int32_t b : order) {
     const int32_t len = context_lens[b];
-    if (len > 0) total += max_items(std::min((len - 1) / kSlots + 1, max_blocks), partition_blocks);
+    const int32_t nblk = std::min((len + kSlots - 1) / kSlots, max_blocks);
+    const int32_t nitems = (nblk + kItemBlocks - 1) / kItemBlocks;
+    const int bin = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
+    load[bin] += nitems;
+    const int32_t* row = block_tables + static_cast<int64_t>(b) * max_blocks;
+    for (int32_t item = 0; item < nitems; ++item) {
+      int32_t rec[kPlanInts] = {b, item, len, nitems};
+      for (int i = 0; i < kItemBlocks; ++i) rec[4 + i] = row[std::min(item * kItemBlocks + i, nblk - 1)];
+      bins[bin].insert(bins[bin].end(), rec, rec + kPlanInts);
+    }
   }
+  int64_t most = 0;
+  for (const auto& v : bins) most = std::max<int64_t>(most, static_cast<int64_t>(v.size()) / kPlanInts);
+  const int64_t total = most * kPlanBins;
   if (total > capacity) {
-    return -set_error(PC_ERR_ARGUMENT, "work item capacity %lld too small (%lld items)",
-                      static_cast<long long>(capacity), static_cast<long long>(total));
+    return -set_error(PC_ERR_ARGUMENT, "plan capacity %lld too small (%lld records)", static_cast<long long>(capacity),
+                      static_cast<long long>(total));
   }
-  // Workgroups are dispatched in record order. A multi-item sequence's closer -- its last
-  // item, the one with the fewest blocks -- goes after every other item of every
-  // sequence, so when it finishes its own blocks its siblings have long published their
-  // partials; before the closers, items with fewer blocks go later.
-  int64_t n = 0;
-  for (int pass = 0; pass < 2; ++pass) {
-    const bool closers = pass == 1;
-    for (int32_t count = partition_blocks; count >= 1; --count) {
-      for (int32_t b = 0; b < batch; ++b) {
-        const int32_t len = context_lens[b];
-        if (len <= 0) continue;
-        const int32_t nblk = std::min((len - 1) / kSlots + 1, max_blocks);
-        const int32_t items = max_items(nblk, partition_blocks);
-        const int32_t* row = block_tables + static_cast<int64_t>(b) * max_blocks;
-        for (int32_t i = 0; i < items; ++i) {
-          const bool closer = items > 1 && i == items - 1;
-          if (closer != closers || std::min(nblk - i * partition_blocks, partition_blocks) != count) continue;
-          int32_t* rec = work_items + n * fields;
-          rec[0] = b;
-          rec[1] = i;
-          rec[2] = len;
-          rec[3] = closer ? 1 : 0;
-          for (int32_t j = 0; j < fields - kPlanHeader; ++j) {
-            const int32_t blk = i * partition_blocks + j;
-            rec[kPlanHeader + j] = (j < count) ? row[blk] : 0;
-          }
-          ++n;
-        }
+  for (int64_t pos = 0; pos < most; ++pos) {
+    for (int x = 0; x < kPlanBins; ++x) {
+      int32_t* dst = plan + (pos * kPlanBins + x) * kPlanInts;
+      if (pos < static_cast<int64_t>(bins[x].size()) / kPlanInts) {
+        std::copy(bins[x].begin() + pos * kPlanInts, bins[x].begin() + (pos + 1) * kPlanInts, dst);
+      } else {
+        std::fill(dst, dst + kPlanInts, 0);
+        dst[0] = -1;
       }
     }
   }
   ok();
-  return static_cast<int32_t>(n);
+  return static_cast<int32_t>(total);
 }
 
 int pc_kv_append(void* pool, int64_t num_blocks, int32_t layer_begin, int32_t num_layers,
@@ -823,63 +766,42 @@ int pc_kv_append(void* pool, int64_t num_blocks, int32_t layer_begin, int32_t nu
   return check_launch("kv_append");
 }
 
-int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t num_blocks,
-                         int32_t layer, const int32_t* block_tables, int32_t max_blocks,
-                         const int32_t* context_lens, int32_t batch, int32_t partition_blocks,
-                         const int32_t* work_items, int32_t num_work_items, void* workspace,
-                         int32_t* tickets, int32_t flags, void* stream) {
-  if (!out || !query || !pool || !block_tables || !context_lens) {
-    return set_error(PC_ERR_ARGUMENT, "null pointer");
-  }
+int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t num_blocks, int32_t layer,
+                         const int32_t* context_lens, int32_t batch, int32_t max_blocks, const int32_t* plan,
+                         int32_t num_records, void* workspace, void* stream) {
+  if (!out || !query || !pool || !context_lens || !plan) return set_error(PC_ERR_ARGUMENT, "null pointer");
   if (num_blocks < 1 || num_blocks > INT32_MAX) return set_error(PC_ERR_ARGUMENT, "num_blocks out of range");
   if (layer < 0 || layer >= kLayers) return set_error(PC_ERR_ARGUMENT, "layer %d outside [0, 22)", layer);
-  if (int rc = check_attn_shape(batch, max_blocks, partition_blocks)) return rc;
-  if (flags & ~PC_ATTN_SEPARATE_REDUCE) return set_error(PC_ERR_ARGUMENT, "unknown flags 0x%x", flags);
-  const int items = max_items(max_blocks, partition_blocks);
-  if (items > 1 && !workspace) return set_error(PC_ERR_ARGUMENT, "workspace required");
-  if (items > 1 && !(flags & PC_ATTN_SEPARATE_REDUCE) && !tickets) {
-    return set_error(PC_ERR_ARGUMENT, "tickets required for the fused merge");
-  }
+  if (int rc = check_attn_shape(batch, max_blocks)) return rc;
+  const int64_t max_items = items_per_sequence(max_blocks);
+  if (max_items > 1 && !workspace) return set_error(PC_ERR_ARGUMENT, "workspace required");
   if (!aligned(query, 16) || !aligned(out, 16) || !aligned(pool, 16) || !aligned(workspace, 256) ||
-      !aligned(tickets, 4) || !aligned(work_items, 4)) {
-    return set_error(PC_ERR_ARGUMENT,
-                     "query/out/pool must be 16-byte, tickets/work_items 4-byte, workspace 256-byte aligned");
+      !aligned(plan, 16) || !aligned(context_lens, 4)) {
+    return set_error(PC_ERR_ARGUMENT, "query/out/pool/plan must be 16-byte, workspace 256-byte aligned");
   }
-  if (work_items && (num_work_items < 0 || num_work_items > static_cast<int64_t>(batch) * items)) {
-    return set_error(PC_ERR_ARGUMENT, "num_work_items %d outside [0, batch * items]", num_work_items);
+  if (num_records < 0 || num_records > (static_cast<int64_t>(batch) + kPlanBins) * max_items) {
+    return set_error(PC_ERR_ARGUMENT, "num_records %d outside [0, (batch + 8) * items per sequence]", num_records);
   }
-  if (batch == 0 || (work_items && num_work_items == 0)) return ok();
-  const WorkspaceLayout w = workspace_layout(batch, max_blocks, partition_blocks);
-  char* base = static_cast<char*>(workspace);
+  if (batch == 0 || num_records == 0) return ok();
   AttnArgs a;
   a.out = static_cast<_Float16*>(out);
   a.query = static_cast<const _Float16*>(query);
   a.pool = static_cast<const _Float16*>(pool);
   a.num_blocks = num_blocks;
-  a.block_tables = block_tables;
+  a.plan = plan;
   a.context_lens = context_lens;
-  a.ws_out = base ? reinterpret_cast<float*>(base + w.out_offset) : nullptr;
-  a.ws_ml = base ? reinterpret_cast<float*>(base + w.ml_offset) : nullptr;
-  a.tickets = tickets;
-  a.work_items = work_items;
+  a.partials = static_cast<float*>(workspace);
   a.layer = layer;
-  a.max_blocks = max_blocks;
   a.batch = batch;
-  a.max_items = items;
-  a.fused_merge = (flags & PC_ATTN_SEPARATE_REDUCE) ? 0 : 1;
+  a.max_blocks = max_blocks;
+  a.max_items = static_cast<int>(max_items);
   hipStream_t s = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
-  const unsigned grid = static_cast<unsigned>(work_items ? static_cast<int64_t>(num_work_items) : static_cast<int64_t>(batch) * items);
-  switch (partition_blocks) {
-    case 1: launch_items<1>(a, grid, s); break;
-    case 2: launch_items<2>(a, grid, s); break;
-    case 4: launch_items<4>(a, grid, s); break;
-    default: launch_items<8>(a, grid, s); break;
-  }
+  hipLaunchKernelGGL(paged_decode_item_kernel, dim3(static_cast<unsigned>(num_records)), dim3(kItemThreads), 0, s, a);
   if (int rc = check_launch("paged_decode_item")) return rc;
-  if (items > 1 && !a.fused_merge) {
-    hipLaunchKernelGGL(paged_decode_merge_kernel, dim3(static_cast<unsigned>(batch) * kKVHeads),
-                       dim3(kMergeThreads), 0, s, a, static_cast<int>(partition_blocks));
+  if (max_items > 1) {
+    hipLaunchKernelGGL(paged_decode_merge_kernel, dim3(static_cast<unsigned>(batch) * kKVHeads), dim3(kMergeThreads), 0,
+                       s, a);
     return check_launch("paged_decode_merge");
   }
   return PC_OK;

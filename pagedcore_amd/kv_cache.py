@@ -109,13 +109,13 @@ class _HostOnlyWriter:
 @dataclass(slots=True)
 class _DecodeBatch:
     """Device block tables and lengths of one batch of requests, plus their host copies
-    and the per-partition-size decode plans built from them."""
+    and the decode plan built from them (on first use)."""
 
     tables: Tensor
     lengths: Tensor
     host_tables: np.ndarray
     host_lengths: np.ndarray
-    plans: Dict[int, Tensor]
+    plan: Optional[Tensor] = None
 
 
 @dataclass(frozen=True, slots=True)
@@ -428,19 +428,15 @@ class KVAllocator:
         batch = self._gather(request_ids, layer_index)
         return batch.tables, batch.lengths
 
-    def decode_work_items(
-        self, request_ids: Sequence[RequestId], *, layer_index: int, partition_blocks: int
-    ) -> Tensor:
+    def decode_plan(self, request_ids: Sequence[RequestId], *, layer_index: int) -> Tensor:
         """Device decode plan (pc_attn_plan records: row, item, length, block ids) for the
-        batch that gather_block_tables returns, built once per allocator state and
-        partition size from the host tables, so the 22 layers of a decode step share it."""
+        batch that gather_block_tables returns, built once per allocator state from the host
+        tables, so the 22 layers of a decode step share it."""
         batch = self._gather(request_ids, layer_index)
-        items = batch.plans.get(partition_blocks)
-        if items is None:
-            plan = _hip.plan_work_items(batch.host_lengths, batch.host_tables, partition_blocks)
-            items = torch.from_numpy(plan).to(self._pool.device)
-            batch.plans[partition_blocks] = items
-        return items
+        if batch.plan is None:
+            plan = _hip.decode_plan(batch.host_lengths, batch.host_tables)
+            batch.plan = torch.from_numpy(plan).to(self._pool.device)
+        return batch.plan
 
     def _gather(self, request_ids: Sequence[RequestId], layer_index: int) -> _DecodeBatch:
         if not request_ids:
@@ -466,7 +462,6 @@ class KVAllocator:
             torch.from_numpy(lengths).to(self._pool.device),
             tables,
             lengths,
-            {},
         )
         if len(self._table_cache) > 64:
             self._table_cache.clear()

@@ -205,13 +205,12 @@ def test_config1_golden_through_the_c_abi(device):
     out = torch.empty(1, 32, 64, dtype=torch.float16, device=device)
     tables = torch.tensor([w.table], dtype=torch.int32, device=device)
     lens = torch.tensor([128], dtype=torch.int32, device=device)
-    for parts in (1, 2, 4, 8):
-        out.fill_(float("nan"))
-        _hip.paged_decode_attention(out, query, pool, w.layer, tables, lens, partition_blocks=parts)
-        torch.cuda.synchronize()
-        expected = torch.from_numpy(golden["expected_fp64"]).reshape(1, 32, 64)
-        torch.testing.assert_close(out.cpu().double(), expected, atol=2e-3, rtol=2e-3)
-        torch.testing.assert_close(out.cpu(), expected.half(), **TOL)
+    out.fill_(float("nan"))
+    _hip.paged_decode_attention(out, query, pool, w.layer, tables, lens)
+    torch.cuda.synchronize()
+    expected = torch.from_numpy(golden["expected_fp64"]).reshape(1, 32, 64)
+    torch.testing.assert_close(out.cpu().double(), expected, atol=2e-3, rtol=2e-3)
+    torch.testing.assert_close(out.cpu(), expected.half(), **TOL)
 
 
 def _random_pool(device, num_blocks, seed):
@@ -238,19 +237,29 @@ def _oracle_rows(pool, layer, w, queries, rows):
     return out
 
 
-@pytest.mark.parametrize("parts", [1, 2, 4, 8])
-def test_batched_decode_b64_matches_oracle(device, parts):
+def _shuffled_plan(w, seed):
+    """The decode plan with its records (padding included) in a random order: the dispatch
+    order, and so the XCD each item runs on, changes; the answer must not."""
+    plan = _hip.decode_plan(w.lengths, w.tables)
+    order = np.random.default_rng(seed).permutation(plan.shape[0])
+    return np.ascontiguousarray(plan[order])
+
+
+@pytest.mark.parametrize("order", ["binned", "shuffled"])
+def test_batched_decode_b64_matches_oracle(device, order):
     """Batch 64, lengths U{1..2048}, fragmented tables over an 8192-block pool; every row
-    against the oracle restatement and FP64, for several split-K partition sizes."""
-    _say("batched b64 parts", parts)
+    against the oracle restatement and FP64, with the plan as built and with its records
+    shuffled."""
+    _say("batched b64 plan", order)
     w = workloads.batched_decode(batch=64, num_blocks=8192)
     pool = _random_pool(device, w.num_blocks, 11)
     layer = 5
     queries = torch.from_numpy(w.queries(layer)).to(device)
-    out = torch.empty_like(queries)
+    out = torch.full_like(queries, float("nan"))
+    plan = _hip.decode_plan(w.lengths, w.tables) if order == "binned" else _shuffled_plan(w, 3)
     _hip.paged_decode_attention(
         out, queries, pool, layer, torch.from_numpy(w.tables).to(device), torch.from_numpy(w.lengths).to(device),
-        partition_blocks=parts,
+        plan=torch.from_numpy(plan).to(device),
     )
     torch.cuda.synchronize()
     expected = _oracle_rows(pool, layer, w, queries, range(w.batch))
@@ -261,8 +270,9 @@ def test_batched_decode_b64_matches_oracle(device, parts):
 
 
 def test_long_context_b256_full_length(device):
-    """Batch 256 at 2048 tokens (128 blocks each) over a fully shuffled 40000-block pool:
-    rows against the oracle, and every partition size giving the same answer."""
+    """Batch 256 at 2048 tokens (128 blocks each, 15 work items) over a fully shuffled
+    40000-block pool -- several rounds of workgroups: rows against the oracle, and a
+    shuffled plan giving the same bits."""
     _say("b256 long context")
     w = workloads.batched_decode(batch=256, num_blocks=40000, fixed_length=2048, seed=44)
     pool = _random_pool(device, w.num_blocks, 12)
@@ -271,109 +281,79 @@ def test_long_context_b256_full_length(device):
     tables = torch.from_numpy(w.tables).to(device)
     lens = torch.from_numpy(w.lengths).to(device)
     results = {}
-    for parts in (2, 4, 8):
-        out = torch.empty_like(queries)
-        _hip.paged_decode_attention(out, queries, pool, layer, tables, lens, partition_blocks=parts)
-        results[parts] = out
+    for order in ("binned", "shuffled"):
+        plan = _hip.decode_plan(w.lengths, w.tables) if order == "binned" else _shuffled_plan(w, 5)
+        out = torch.full_like(queries, float("nan"))
+        _hip.paged_decode_attention(out, queries, pool, layer, tables, lens, plan=torch.from_numpy(plan).to(device))
+        results[order] = out
     torch.cuda.synchronize()
-    for parts in (2, 8):
-        torch.testing.assert_close(results[parts], results[4], **TOL)
+    assert torch.equal(results["binned"], results["shuffled"])
     expected = _oracle_rows(pool, layer, w, queries, [0, 1, 127, 255])
     for b, (oracle, fp64) in expected.items():
-        got = results[4][b : b + 1].reshape(1, 32, 1, 64).cpu()
+        got = results["binned"][b : b + 1].reshape(1, 32, 1, 64).cpu()
         torch.testing.assert_close(got, oracle, **TOL)
         torch.testing.assert_close(got, fp64, **TOL)
 
 
-def test_fused_merge_equals_separate_reduce_and_rearms_tickets(device):
-    """The last-arriver merge inside the partition kernel gives bit-identical output to the
-    separate reduce kernel, on every call (the tickets return to zero), including inside a
-    replayed HIP graph."""
-    w = workloads.batched_decode(batch=64, num_blocks=8192, seed=48)
-    pool = _random_pool(device, w.num_blocks, 16)
-    queries = torch.from_numpy(w.queries(7)).to(device)
-    tables = torch.from_numpy(w.tables).to(device)
-    lens = torch.from_numpy(w.lengths).to(device)
-    for parts in (1, 4, 8):
-        nbytes = _hip.workspace_bytes(w.batch, tables.shape[1], parts)
-        workspace = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=device)  # scratch: contents irrelevant
-        tickets = torch.zeros(w.batch, dtype=torch.int32, device=device)
-        separate = torch.empty_like(queries)
-        _hip.paged_decode_attention(separate, queries, pool, 7, tables, lens, partition_blocks=parts, workspace=workspace, tickets=tickets, separate_reduce=True)
-        for _ in range(3):
-            fused = torch.full_like(queries, float("nan"))
-            _hip.paged_decode_attention(fused, queries, pool, 7, tables, lens, partition_blocks=parts, workspace=workspace, tickets=tickets, separate_reduce=False)
-            torch.cuda.synchronize()
-            assert torch.equal(fused, separate), parts
-        assert torch.count_nonzero(tickets) == 0
-        graph_out = torch.empty_like(queries)
-        side = torch.cuda.Stream(device=device)
-        side.wait_stream(torch.cuda.current_stream(device))
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(side), torch.cuda.graph(graph, stream=side):
-            _hip.paged_decode_attention(graph_out, queries, pool, 7, tables, lens, partition_blocks=parts, workspace=workspace, tickets=tickets, separate_reduce=False)
-        torch.cuda.current_stream(device).wait_stream(side)
-        for _ in range(3):
-            graph_out.fill_(float("nan"))
-            graph.replay()
-            torch.cuda.synchronize()
-            assert torch.equal(graph_out, separate), parts
-        assert torch.count_nonzero(tickets) == 0
-
-
-@pytest.mark.parametrize("separate", [False, True])
-def test_planned_grid_equals_full_grid(device, separate):
-    """The host plan (only partitions that exist) gives bit-identical output to the full
-    partition-slot grid, for ragged lengths with empty-tail rows, several partition
-    sizes, both merge modes, and inside replayed HIP graphs."""
-    _say("planned grid, separate", separate)
+def test_plan_order_and_graph_replays_are_invisible(device):
+    """Ragged lengths with empty, one-token, block-boundary and full rows: the output is the
+    same bits for the plan as built, for its records reversed, and for every replay of a
+    captured HIP graph (with eager calls in between), and matches the oracle."""
+    _say("plan order and graph replays")
     w = workloads.batched_decode(batch=64, num_blocks=8192, seed=49)
     lengths = w.lengths.copy()
-    lengths[:4] = [1, 16, 17, 2048]
+    lengths[:6] = [1, 16, 17, 144, 145, 2048]
+    lengths[6] = 0  # no cached token: the row is not written
     pool = _random_pool(device, w.num_blocks, 18)
     queries = torch.from_numpy(w.queries(9)).to(device)
     tables = torch.from_numpy(w.tables).to(device)
     lens = torch.from_numpy(lengths).to(device)
-    for parts in (1, 2, 4, 8):
-        items = torch.from_numpy(_hip.plan_work_items(lengths, w.tables, parts)).to(device)
-        full = torch.full_like(queries, float("nan"))
-        _hip.paged_decode_attention(full, queries, pool, 9, tables, lens, partition_blocks=parts, separate_reduce=separate)
-        planned = torch.full_like(queries, float("nan"))
-        _hip.paged_decode_attention(planned, queries, pool, 9, tables, lens, partition_blocks=parts, work_items=items, separate_reduce=separate)
+    plan = _hip.decode_plan(lengths, w.tables)
+    first = torch.full_like(queries, 7.0)
+    _hip.paged_decode_attention(first, queries, pool, 9, tables, lens, plan=torch.from_numpy(plan).to(device))
+    reversed_out = torch.full_like(queries, 7.0)
+    _hip.paged_decode_attention(
+        reversed_out, queries, pool, 9, tables, lens, plan=torch.from_numpy(np.ascontiguousarray(plan[::-1])).to(device)
+    )
+    torch.cuda.synchronize()
+    assert torch.equal(first, reversed_out)
+    assert torch.equal(first[6], torch.full_like(first[6], 7.0))  # untouched
+    live = [b for b in range(64) if b != 6]
+    assert not torch.isnan(first[live]).any()
+    device_plan = torch.from_numpy(plan).to(device)
+    graph_out = torch.empty_like(queries)
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side), torch.cuda.graph(graph, stream=side):
+        _hip.paged_decode_attention(graph_out, queries, pool, 9, tables, lens, plan=device_plan)
+    torch.cuda.current_stream(device).wait_stream(side)
+    for _ in range(3):
+        graph_out.fill_(float("nan"))
+        graph.replay()
         torch.cuda.synchronize()
-        assert torch.equal(planned, full), parts
-        assert not torch.isnan(planned).any()
-        graph_out = torch.empty_like(queries)
-        side = torch.cuda.Stream(device=device)
-        side.wait_stream(torch.cuda.current_stream(device))
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(side), torch.cuda.graph(graph, stream=side):
-            _hip.paged_decode_attention(graph_out, queries, pool, 9, tables, lens, partition_blocks=parts, work_items=items, separate_reduce=separate)
-        torch.cuda.current_stream(device).wait_stream(side)
-        for _ in range(3):
-            graph_out.fill_(float("nan"))
-            graph.replay()
-            torch.cuda.synchronize()
-            assert torch.equal(graph_out, full), parts
-    rows = [0, 1, 2, 3, 40]
+        assert torch.equal(graph_out[live], first[live])
+        eager = torch.empty_like(queries)
+        _hip.paged_decode_attention(eager, queries, pool, 9, tables, lens, plan=device_plan)
+        torch.cuda.synchronize()
+        assert torch.equal(eager[live], first[live])
     w.lengths = lengths
-    for b, (oracle, fp64) in _oracle_rows(pool, 9, w, queries, rows).items():
-        got = planned[b : b + 1].reshape(1, 32, 1, 64).cpu()
+    for b, (oracle, fp64) in _oracle_rows(pool, 9, w, queries, [0, 1, 2, 3, 4, 5, 40]).items():
+        got = first[b : b + 1].reshape(1, 32, 1, 64).cpu()
         torch.testing.assert_close(got, oracle, **TOL)
         torch.testing.assert_close(got, fp64, **TOL)
 
 
 def test_cached_scratch_survives_changing_shapes(device):
-    """Calls of different batch sizes, table widths and partition sizes share the cached
-    per-stream scratch; each must still match the oracle."""
+    """Calls of different batch sizes and table widths share the cached per-stream scratch;
+    each must still match the oracle."""
     pool = _random_pool(device, 1024, 17)
-    for batch, hi, parts, layer in ((3, 300, 4, 1), (9, 1000, 2, 2), (2, 2048, 1, 3), (9, 900, 8, 4)):
+    for batch, hi, layer in ((3, 300, 1), (9, 1000, 2), (2, 2048, 3), (9, 900, 4)):
         w = workloads.batched_decode(batch=batch, lo=20, hi=hi, num_blocks=1024, seed=batch + hi)
         queries = torch.from_numpy(w.queries(layer)).to(device)
         out = torch.full_like(queries, float("nan"))
         _hip.paged_decode_attention(
-            out, queries, pool, layer, torch.from_numpy(w.tables).to(device), torch.from_numpy(w.lengths).to(device),
-            partition_blocks=parts,
+            out, queries, pool, layer, torch.from_numpy(w.tables).to(device), torch.from_numpy(w.lengths).to(device)
         )
         torch.cuda.synchronize()
         for b, (oracle, fp64) in _oracle_rows(pool, layer, w, queries, range(batch)).items():

@@ -33,15 +33,15 @@ def test_library_exports_every_declared_symbol():
 
 def test_workspace_size_formula():
     lib = _hip.load()
-    # partials: 64 sequences x ceil(128/4) items x 32 q heads x 64 floats, then the
-    # (max, sum) pairs; 256 B aligned regions
-    out = 64 * 32 * 32 * 64 * 4
-    ml = 64 * 32 * 32 * 2 * 4
-    assert lib.pc_attn_workspace_bytes(64, 128, 4) == out + ml
-    assert lib.pc_attn_workspace_bytes(1, 8, 4) == 2 * 32 * 64 * 4 + 512
-    assert lib.pc_attn_workspace_bytes(1, 9, 8) == lib.pc_attn_workspace_bytes(1, 8, 4)
-    for bad in (0, 3, 5, 16, 64):  # items hold 1, 2, 4 or 8 blocks
-        assert lib.pc_attn_workspace_bytes(1, 8, bad) == 0
+    # one fp32 partial per (sequence, kv head, 9-block work item): O [8 q heads][64] then
+    # (max, sum) of the 8 q heads
+    part = (8 * 64 + 16) * 4
+    assert lib.pc_attn_workspace_bytes(64, 128) == 64 * 4 * 15 * part
+    assert lib.pc_attn_workspace_bytes(1, 9) == 4 * part
+    assert lib.pc_attn_workspace_bytes(1, 10) == 4 * 2 * part
+    assert lib.pc_attn_workspace_bytes(0, 128) == 0
+    for batch, blocks in ((-1, 8), (1, 0), (1, 65537)):
+        assert lib.pc_attn_workspace_bytes(batch, blocks) == 0
 
 
 @pytest.mark.parametrize(
@@ -66,100 +66,100 @@ def test_append_rejects_invalid_arguments_without_a_gpu(args, needle):
         ({"layer": 22}, b"layer"),
         ({"batch": -1}, b"batch"),
         ({"max_blocks": 0}, b"max_blocks"),
-        ({"parts": 0}, b"partition_blocks"),
-        ({"parts": 3}, b"partition_blocks"),
-        ({"parts": 16}, b"partition_blocks"),
+        ({"plan": None}, b"null pointer"),
+        ({"lens": None}, b"null pointer"),
         ({"ws": None}, b"workspace"),
         ({"ws": 272}, b"aligned"),
         ({"query": 8}, b"aligned"),
         ({"out": 260}, b"aligned"),
-        ({"flags": 6}, b"flags"),
-        ({"tickets": None}, b"tickets"),
-        ({"tickets": 258}, b"aligned"),
+        ({"plan": 260}, b"aligned"),
         ({"blocks": 2**31}, b"num_blocks"),
-        ({"items": 258}, b"aligned"),
-        ({"items": 256, "nitems": -1}, b"num_work_items"),
-        ({"items": 256, "nitems": 17}, b"num_work_items"),  # batch 1 x 16 items
+        ({"nrec": -1}, b"num_records"),
+        ({"nrec": (1 + 8) * 15 + 1}, b"num_records"),  # batch 1, 128 blocks: 15 items per sequence
     ],
 )
 def test_attention_rejects_invalid_arguments_without_a_gpu(overrides, needle):
     lib = _hip.load()
-    a = {"out": 256, "query": 256, "pool": 256, "blocks": 10, "layer": 0, "tables": 256, "max_blocks": 128,
-         "lens": 256, "batch": 1, "parts": 8, "items": None, "nitems": 0, "ws": 256, "tickets": 256, "flags": 0}
+    a = {"out": 256, "query": 256, "pool": 256, "blocks": 10, "layer": 0, "lens": 256, "batch": 1,
+         "max_blocks": 128, "plan": 256, "nrec": 1, "ws": 256}
     a.update(overrides)
     status = lib.pc_paged_decode_attn(
-        a["out"], a["query"], a["pool"], a["blocks"], a["layer"], a["tables"], a["max_blocks"], a["lens"],
-        a["batch"], a["parts"], a["items"], a["nitems"], a["ws"], a["tickets"], a["flags"], None,
+        a["out"], a["query"], a["pool"], a["blocks"], a["layer"], a["lens"], a["batch"], a["max_blocks"],
+        a["plan"], a["nrec"], a["ws"], None,
     )
     assert status == 1
     assert needle in lib.pc_last_error()
 
 
-def _plan_by_enumeration(lengths, tables, partition_blocks):
-    """The plan records written out directly: {row, item, length, 0 (closer flag, set by
-    the caller), block ids padded with 0 to a multiple of 4}."""
-    fields = 4 + -(-partition_blocks // 4) * 4
-    rows = []
+def _items_by_enumeration(lengths, tables):
+    """Every (sequence, item) record written out directly: {row, item, length, items of the
+    row, the item's 9 block ids (past the row's last block: its last id), 0, 0, 0}."""
+    records = {}
     for b, length in enumerate(lengths):
         if length <= 0:
             continue
         blocks = min(-(-int(length) // 16), tables.shape[1])
-        for item in range(-(-blocks // partition_blocks)):
-            ids = [int(tables[b, i]) for i in range(item * partition_blocks, min((item + 1) * partition_blocks, blocks))]
-            record = [b, item, int(length), 0] + ids
-            rows.append(tuple(record + [0] * (fields - len(record))))
-    return rows
+        items = -(-blocks // 9)
+        for item in range(items):
+            ids = [int(tables[b, min(item * 9 + i, blocks - 1)]) for i in range(9)]
+            records[(b, item)] = tuple([b, item, int(length), items] + ids + [0, 0, 0])
+    return records
 
 
-@pytest.mark.parametrize("partition_blocks", [1, 2, 4, 8])
-def test_decode_plan_lists_every_partition_once(partition_blocks):
+def test_decode_plan_lists_every_item_once_on_one_bin_per_sequence():
     """pc_attn_plan (host code) against a direct enumeration, on ragged lengths including
-    zero-length rows, exact block multiples and lengths clamped by the table width."""
-    rng = np.random.default_rng(partition_blocks)
+    zero-length rows, exact block multiples and lengths clamped by the table width: every
+    item appears once, the items of a sequence share record index modulo 8 (one XCD), the
+    8 bins' item counts differ by at most one sequence's items, padding records are empty,
+    and longer sequences are dealt first."""
+    rng = np.random.default_rng(5)
     lengths = rng.integers(0, 2049, size=97).astype(np.int32)
     lengths[:6] = [0, 1, 16, 17, 2048, 5000]  # 5000 tokens exceed the 128-block width: clamped
     tables = rng.integers(0, 50000, size=(97, 128)).astype(np.int32)
-    plan = _hip.plan_work_items(lengths, tables, partition_blocks)
-    assert plan.dtype == np.int32 and plan.shape[1] == _hip.load().pc_attn_plan_record_ints(partition_blocks)
-    records = [tuple(r) for r in plan.tolist()]
-    expected = _plan_by_enumeration(lengths, tables, partition_blocks)
-    # the closer flag marks the last item of every multi-item sequence
-    items_of = {}
-    for r in expected:
-        items_of[r[0]] = items_of.get(r[0], 0) + 1
-    expected = [r[:3] + (1 if items_of[r[0]] > 1 and r[1] == items_of[r[0]] - 1 else 0,) + r[4:] for r in expected]
-    assert sorted(records) == sorted(expected)
-    # dispatch order: every closer after every other item; within each group, items with
-    # more blocks first, sequence-major among equals
-    flags = [r[3] for r in records]
-    assert flags == sorted(flags)
-    for flag in (0, 1):
-        group = [r for r in records if r[3] == flag]
-        counts = [min(min(-(-r[2] // 16), 128) - r[1] * partition_blocks, partition_blocks) for r in group]
-        assert counts == sorted(counts, reverse=True)
-        for count in set(counts):
-            rows = [(r[0], r[1]) for r, c in zip(group, counts) if c == count]
-            assert rows == sorted(rows)
+    plan = _hip.decode_plan(lengths, tables)
+    lib = _hip.load()
+    assert plan.dtype == np.int32 and plan.shape[1] == lib.pc_attn_plan_record_ints() == 16
+    assert plan.shape[0] % 8 == 0 and plan.shape[0] <= lib.pc_attn_plan_capacity(97, 128)
+    expected = _items_by_enumeration(lengths, tables)
+    live = [tuple(r) for r in plan.tolist() if r[0] >= 0]
+    assert sorted(live) == sorted(expected.values())
+    for r in plan.tolist():
+        if r[0] < 0:
+            assert r == [-1] + [0] * 15
+    bin_of = {}
+    for index, r in enumerate(plan.tolist()):
+        if r[0] >= 0:
+            assert bin_of.setdefault(r[0], index % 8) == index % 8, "items of a sequence on two bins"
+    per_bin = [sum(1 for index, r in enumerate(plan.tolist()) if r[0] >= 0 and index % 8 == x) for x in range(8)]
+    assert max(per_bin) - min(per_bin) <= 15
+    first_seen = {}
+    for index, r in enumerate(plan.tolist()):
+        if r[0] >= 0:
+            first_seen.setdefault(r[0], index // 8)
+    # within a bin, rows appear in order of decreasing length
+    for x in range(8):
+        rows = sorted((first_seen[b], b) for b in bin_of if bin_of[b] == x)
+        lens = [lengths[b] for _, b in rows]
+        assert lens == sorted(lens, reverse=True)
 
 
 def test_decode_plan_rejects_bad_arguments():
     lib = _hip.load()
     lens = np.array([100, 200], dtype=np.int32)
     tables = np.zeros((2, 16), dtype=np.int32)
-    items = np.zeros((2, 8), dtype=np.int32)
+    records = np.zeros((64, 16), dtype=np.int32)
     plan = lib.pc_attn_plan
-    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, 4, items.ctypes.data, 2) == -1  # needs 2 + 4 records
+    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, records.ctypes.data, 8) == -1  # needs 16 records
     assert b"capacity" in lib.pc_last_error()
-    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, 0, items.ctypes.data, 2) == -1
-    assert b"partition_blocks" in lib.pc_last_error()
-    assert plan(None, tables.ctypes.data, 2, 16, 4, items.ctypes.data, 2) == -1
-    assert plan(lens.ctypes.data, None, 2, 16, 4, items.ctypes.data, 2) == -1
+    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, records.ctypes.data, 16) == 16
+    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 0, records.ctypes.data, 64) == -1
+    assert b"max_blocks" in lib.pc_last_error()
+    assert plan(None, tables.ctypes.data, 2, 16, records.ctypes.data, 64) == -1
+    assert plan(lens.ctypes.data, None, 2, 16, records.ctypes.data, 64) == -1
     assert b"null" in lib.pc_last_error()
-    assert lib.pc_attn_plan_capacity(2, 16, 4) == 8
-    assert lib.pc_attn_plan_capacity(2, 16, 6) == -1
-    assert [lib.pc_attn_plan_record_ints(w) for w in (1, 2, 4, 8)] == [8, 8, 8, 12]
-    assert lib.pc_attn_plan_record_ints(3) == -1
-    assert plan(None, None, 0, 16, 4, None, 0) == 0  # empty batch: nothing to plan
+    assert lib.pc_attn_plan_capacity(2, 16) == (2 + 8) * 2
+    assert lib.pc_attn_plan_capacity(2, 0) == -1
+    assert plan(None, None, 0, 16, None, 0) == 0  # empty batch: nothing to plan
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
