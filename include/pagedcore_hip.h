@@ -116,6 +116,65 @@ int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, i
 int32_t pc_attn_plan_record_ints(void);
 int64_t pc_attn_plan_capacity(int32_t batch, int32_t max_blocks);
 
+/*
+ * Decode-step kernels around paged attention. Each one rounds to fp16 exactly where the
+ * reference's torch expression materialises an fp16 tensor (every fp16 torch op computes in
+ * fp32 and rounds its result once), so only fp32 reduction order differs from the reference.
+ */
+
+/*
+ * RoPE on one token's query and key, fused with the KV append of its rotated key and
+ * unrotated value.
+ *
+ * Replaces apply_rope (reference src/pagedcore/dense.py:33-61) on decode and prefill
+ * tokens, and the per-row KVAllocator.write_decode_layer copies of the rotated key and the
+ * value (reference src/pagedcore/kv_cache.py:221-246, called at src/pagedcore/decoder.py:185-187).
+ *
+ *   qkv          [num_tokens][qkv_stride] fp16: columns 0..2047 are the 32 query heads,
+ *                2048..2303 the 4 key heads, 2304..2559 the 4 value heads (qkv_stride >= 2560,
+ *                a multiple of 8)
+ *   positions    [num_tokens] int64: the token's absolute position, in [0, rope_positions)
+ *   rope_table   [rope_positions][2][32] fp16: cos, then sin, of position * inv_freq[j] with
+ *                inv_freq[j] = 1 / 10000^(2j / 64), computed in fp32 and rounded to fp16
+ *   query_out    [num_tokens][32][64] fp16: the rotated queries
+ *   key_out, value_out  [num_tokens][4][64] fp16 or null: the rotated keys / the values
+ *   pool, slot_mapping  both null, or the KV pool and [num_tokens] int64 slots
+ *                (block * 16 + offset; negative or >= num_blocks * 16: the token is not
+ *                written): the rotated key and the value go to pool[layer][0 / 1][slot]
+ *
+ * For each head x and d < 32 (c, s the table row of the token's position):
+ *   out[d]      = fp16(fp16(x[d] * c[d])      + fp16(-x[d + 32] * s[d]))
+ *   out[d + 32] = fp16(fp16(x[d + 32] * c[d]) + fp16(x[d] * s[d]))
+ * All buffers 16-byte aligned. A position outside the table is rejected by the callers;
+ * inside the kernel it turns the token's rows to NaN and skips its pool write.
+ */
+int pc_rope_kv_append(void* query_out, void* key_out, void* value_out, const void* qkv, int64_t qkv_stride,
+                      const int64_t* positions, const void* rope_table, int32_t rope_positions, void* pool,
+                      int64_t num_blocks, int32_t layer, const int64_t* slot_mapping, int64_t num_tokens,
+                      void* stream);
+
+/*
+ * Residual add fused with RMSNorm, over rows of `width` fp16 (a multiple of 8, <= 8192).
+ *
+ * Replaces the residual sums of the decoder (reference src/pagedcore/decoder.py:191-192 and
+ * :238-239) followed by rms_norm (reference src/pagedcore/dense.py:17-21):
+ *   if delta is not null: hidden = fp16(hidden + delta)   (in place)
+ *   out = fp16(weight * fp16(hidden * rsqrt(mean(hidden^2) + eps)))   (mean in fp32)
+ * hidden, delta, out: [rows][width]; weight: [width]; all 16-byte aligned; out must not
+ * overlap hidden or delta.
+ */
+int pc_add_rms_norm(void* out, void* hidden, const void* delta, const void* weight, int64_t rows, int32_t width,
+                    float eps, void* stream);
+
+/*
+ * SwiGLU activation. Replaces the elementwise part of swiglu
+ * (reference src/pagedcore/dense.py:102-104):
+ *   out[r][i] = fp16(fp16(silu(gate_up[r][i])) * gate_up[r][width + i]),  silu(x) = x / (1 + e^-x)
+ * gate_up: [rows][2 * width] (the gate projection's outputs, then the up projection's);
+ * out: [rows][width]; width a multiple of 8; both 16-byte aligned.
+ */
+int pc_silu_mul(void* out, const void* gate_up, int64_t rows, int32_t width, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

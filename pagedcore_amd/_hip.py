@@ -17,7 +17,7 @@ import numpy as np
 import torch
 from torch import Tensor
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 LIBRARY_NAME = "libpagedcore_hip.so"
 
 _lock = threading.Lock()
@@ -53,6 +53,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pc_attn_plan_record_ints.argtypes = []
     lib.pc_attn_plan_capacity.restype = _i64
     lib.pc_attn_plan_capacity.argtypes = [_i32, _i32]
+    lib.pc_rope_kv_append.restype = ctypes.c_int
+    lib.pc_rope_kv_append.argtypes = [_p, _p, _p, _p, _i64, _p, _p, _i32, _p, _i64, _i32, _p, _i64, _p]
+    lib.pc_add_rms_norm.restype = ctypes.c_int
+    lib.pc_add_rms_norm.argtypes = [_p, _p, _p, _p, _i64, _i32, ctypes.c_float, _p]
+    lib.pc_silu_mul.restype = ctypes.c_int
+    lib.pc_silu_mul.argtypes = [_p, _p, _i64, _i32, _p]
 
 
 def load() -> ctypes.CDLL:
@@ -219,3 +225,68 @@ def paged_decode_attention(
         _stream(pool.device),
     )
     _check(lib, "pc_paged_decode_attn", status)
+
+
+def _ptr(tensor: Optional[Tensor]) -> Optional[int]:
+    return None if tensor is None else tensor.data_ptr()
+
+
+def rope_kv_append(
+    query_out: Tensor,
+    qkv: Tensor,
+    positions: Tensor,
+    rope_table: Tensor,
+    *,
+    key_out: Optional[Tensor] = None,
+    value_out: Optional[Tensor] = None,
+    pool: Optional[Tensor] = None,
+    layer: int = 0,
+    slot_mapping: Optional[Tensor] = None,
+) -> None:
+    """RoPE on each token's query and key; the rotated key and the value optionally go to
+    key_out/value_out and to pool[layer, 0/1, slot // 16, slot % 16].
+
+    qkv: fp16 [tokens, >= 2560] with unit column stride (q | k | v columns); positions:
+    int64 [tokens]; rope_table: fp16 [positions, 2, 32]; query_out: fp16 [tokens, 32, 64];
+    key_out/value_out: fp16 [tokens, 4, 64]; slot_mapping: int64 [tokens]. All contiguous
+    except qkv's row stride, on one device; enqueued on its current stream. Positions are
+    not read back here: callers check them on the host.
+    """
+    lib = load()
+    if qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise HipExtensionError("qkv must be [tokens, columns] with unit column stride")
+    status = lib.pc_rope_kv_append(
+        query_out.data_ptr(),
+        _ptr(key_out),
+        _ptr(value_out),
+        qkv.data_ptr(),
+        qkv.stride(0),
+        positions.data_ptr(),
+        rope_table.data_ptr(),
+        rope_table.shape[0],
+        _ptr(pool),
+        pool.shape[2] if pool is not None else 0,
+        layer,
+        _ptr(slot_mapping),
+        qkv.shape[0],
+        _stream(qkv.device),
+    )
+    _check(lib, "pc_rope_kv_append", status)
+
+
+def add_rms_norm(out: Tensor, hidden: Tensor, delta: Optional[Tensor], weight: Tensor, eps: float = 1e-5) -> None:
+    """hidden += delta (fp16, in place, when delta is given); out = RMSNorm(hidden) * weight.
+    hidden/delta/out: contiguous fp16 [rows, width]; weight fp16 [width]."""
+    lib = load()
+    status = lib.pc_add_rms_norm(
+        out.data_ptr(), hidden.data_ptr(), _ptr(delta), weight.data_ptr(), hidden.shape[0], hidden.shape[1], eps,
+        _stream(hidden.device),
+    )
+    _check(lib, "pc_add_rms_norm", status)
+
+
+def silu_mul(out: Tensor, gate_up: Tensor) -> None:
+    """out = fp16(fp16(silu(gate)) * up) for gate_up = [gate | up], contiguous fp16 [rows, 2 * width]."""
+    lib = load()
+    status = lib.pc_silu_mul(out.data_ptr(), gate_up.data_ptr(), out.shape[0], out.shape[1], _stream(out.device))
+    _check(lib, "pc_silu_mul", status)

@@ -9,7 +9,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 PACKAGE = os.path.dirname(HERE)
 ROOT = os.path.dirname(PACKAGE)
-SOURCE = os.path.join(HERE, "pagedcore_hip.hip")
+SOURCES = [os.path.join(HERE, name) for name in ("pagedcore_hip.hip", "decode_step.hip")]
 OUTPUT = os.path.join(PACKAGE, "libpagedcore_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -34,7 +34,7 @@ FLAGS = [
 
 def build(verbose: bool = False) -> str:
     tmp = OUTPUT + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, SOURCE]
+    cmd = [HIPCC, *FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, *SOURCES]
     result = subprocess.run(cmd, capture_output=True, text=True)
     noise = "packed-fp32-ops' is not a recognized feature"
     messages = [line for line in (result.stdout + result.stderr).splitlines() if noise not in line]

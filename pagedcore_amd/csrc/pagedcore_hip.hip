@@ -19,21 +19,13 @@
 #include <stdio.h>
 
 #include "pagedcore_hip.h"
+#include "pc_internal.h"
+
+namespace pc_internal {
 
 namespace {
-
-constexpr int kAbiVersion = 7;
-constexpr int kLayers = 22;
-constexpr int kSlots = 16;
-constexpr int kKVHeads = 4;
-constexpr int kQHeads = 32;
-constexpr int kGroup = kQHeads / kKVHeads;  // 8 query heads per kv head
-constexpr int kHeadDim = 64;
-constexpr int64_t kRowElems = kKVHeads * kHeadDim;  // 256 fp16 per token row
-constexpr int64_t kBlockElems = kSlots * kRowElems;  // 4096 fp16 per (layer, kind, block)
-constexpr int kRowChunks = kRowElems * 2 / 16;       // 32 chunks of 16 B per token row
-
 thread_local char g_error[512] = "";
+}  // namespace
 
 int set_error(int code, const char* fmt, ...) {
   va_list args;
@@ -55,6 +47,28 @@ int check_launch(const char* what) {
   }
   return ok();
 }
+
+const char* last_error() { return g_error; }
+
+}  // namespace pc_internal
+
+namespace {
+
+using pc_internal::aligned;
+using pc_internal::check_launch;
+using pc_internal::ok;
+using pc_internal::set_error;
+
+constexpr int kAbiVersion = 8;
+constexpr int kLayers = 22;
+constexpr int kSlots = 16;
+constexpr int kKVHeads = 4;
+constexpr int kQHeads = 32;
+constexpr int kGroup = kQHeads / kKVHeads;  // 8 query heads per kv head
+constexpr int kHeadDim = 64;
+constexpr int64_t kRowElems = kKVHeads * kHeadDim;  // 256 fp16 per token row
+constexpr int64_t kBlockElems = kSlots * kRowElems;  // 4096 fp16 per (layer, kind, block)
+constexpr int kRowChunks = kRowElems * 2 / 16;       // 32 chunks of 16 B per token row
 
 // ---------------------------------------------------------------------------------------
 // KV append: token rows -> pool slots. Raw 16-bit moves only, so the copy is bit-exact.
@@ -638,15 +652,13 @@ int check_attn_shape(int32_t batch, int32_t max_blocks) {
   return PC_OK;
 }
 
-bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
-
 }  // namespace
 
 extern "C" {
 
 int pc_abi_version(void) { return kAbiVersion; }
 
-const char* pc_last_error(void) { return g_error; }
+const char* pc_last_error(void) { return pc_internal::last_error(); }
 
 int32_t pc_attn_plan_record_ints(void) { return kPlanInts; }
 

@@ -1,0 +1,360 @@
+"""Batched TinyLlama decode step and paged prefill over the paged KV pool.
+
+Drop-in for the paged callers of the reference decoder: ``decode_paged``
+(src/pagedcore/decoder.py:156-199) and ``prefill_paged`` (:113-135) keep their signatures,
+argument checks, error types, staged-append semantics and output shapes. The weights
+mirror src/pagedcore/weights.py:51-69 field for field.
+
+What changes is the shape of the work. The reference decodes row by row ("single-request
+shapes", decoder.py:183) with about twenty tiny launches per row and layer. Here one
+decode step is one batch-wide pass per layer:
+
+  x      = RMSNorm(embedding[ids])                           pc_add_rms_norm
+  per layer:
+    qkv  = x @ [Wq; Wk; Wv]^T                                 fp16 GEMM (hipBLASLt via torch)
+    q    = RoPE(q); RoPE(k) and v -> the staged pool slots     pc_rope_kv_append
+    a    = paged attention(q) over the request's blocks        pc_paged_decode_attn
+    h   += a @ Wo^T;  x = RMSNorm(h)                           GEMM, pc_add_rms_norm
+    m    = silu(x @ Wgate^T) * (x @ Wup^T)                     one GEMM on [Wgate; Wup], pc_silu_mul
+    h   += m @ Wdown^T; x = RMSNorm_next(h)                    GEMM, pc_add_rms_norm
+  logits = x @ Wlm^T                                          GEMM
+
+Every elementwise kernel rounds to fp16 where the reference's torch expression does (see
+the kernels' comments), so a row's result differs from the reference only by fp32
+summation order inside the GEMMs, the norms and the attention.
+"""
+
+from __future__ import annotations
+
+import weakref
+from dataclasses import dataclass
+from typing import Dict, Optional, Sequence, Tuple
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from pagedcore_amd import _hip
+from pagedcore_amd.attention import paged_attention_batch
+from pagedcore_amd.engine_types import RequestId
+from pagedcore_amd.kv_cache import CONTEXT_LIMIT, HEAD_DIM, KV_HEADS, LAYERS, KVAllocator
+
+Q_HEADS = 32
+HIDDEN = Q_HEADS * HEAD_DIM  # 2048
+KV_WIDTH = KV_HEADS * HEAD_DIM  # 256
+QKV_WIDTH = HIDDEN + 2 * KV_WIDTH  # 2560
+INTERMEDIATE = 5632
+VOCAB = 32000
+RMS_EPS = 1e-5
+ROPE_THETA = 10000.0
+
+
+@dataclass(frozen=True, eq=False)
+class LayerWeights:
+    """One decoder layer's fp16 weights (reference src/pagedcore/weights.py:51-61)."""
+
+    input_norm: Tensor  # [2048]
+    q_proj: Tensor  # [2048, 2048]
+    k_proj: Tensor  # [256, 2048]
+    v_proj: Tensor  # [256, 2048]
+    o_proj: Tensor  # [2048, 2048]
+    post_attention_norm: Tensor  # [2048]
+    gate_proj: Tensor  # [intermediate, 2048]
+    up_proj: Tensor  # [intermediate, 2048]
+    down_proj: Tensor  # [2048, intermediate]
+
+
+@dataclass(frozen=True, eq=False)
+class TinyLlamaWeights:
+    """Embedding, layers, final norm and untied LM head (reference weights.py:64-69)."""
+
+    embedding: Tensor  # [vocab, 2048]
+    layers: Tuple[LayerWeights, ...]
+    final_norm: Tensor  # [2048]
+    lm_head: Tensor  # [vocab, 2048]
+
+
+# ---------------------------------------------------------------------------------------
+# Weights
+# ---------------------------------------------------------------------------------------
+
+
+def _rows_view(parts: Sequence[Tensor]) -> Optional[Tensor]:
+    """The [sum of rows, columns] tensor that `parts` already form in memory, if they are
+    contiguous row blocks laid end to end in one storage; else None."""
+    first = parts[0]
+    expected = first.data_ptr()
+    for part in parts:
+        if (
+            part.dim() != 2
+            or not part.is_contiguous()
+            or part.shape[1] != first.shape[1]
+            or part.dtype != first.dtype
+            or part.device != first.device
+            or part.untyped_storage().data_ptr() != first.untyped_storage().data_ptr()
+            or part.data_ptr() != expected
+        ):
+            return None
+        expected += part.numel() * part.element_size()
+    rows = sum(part.shape[0] for part in parts)
+    return first.new_empty(0).set_(first.untyped_storage(), first.storage_offset(), (rows, first.shape[1]), (first.shape[1], 1))
+
+
+@dataclass(frozen=True)
+class _FusedLayer:
+    qkv: Tensor  # [2560, 2048]: q_proj | k_proj | v_proj rows
+    gate_up: Tensor  # [2 * intermediate, 2048]: gate_proj | up_proj rows
+
+
+_fused_cache: "weakref.WeakKeyDictionary[LayerWeights, _FusedLayer]" = weakref.WeakKeyDictionary()
+
+
+def _fused(layer: LayerWeights) -> _FusedLayer:
+    """The layer's stacked projection matrices: views when the weights were allocated
+    stacked (random_weights, pack_weights), else one concatenated copy kept per layer."""
+    cached = _fused_cache.get(layer)
+    if cached is None:
+        qkv = _rows_view((layer.q_proj, layer.k_proj, layer.v_proj))
+        gate_up = _rows_view((layer.gate_proj, layer.up_proj))
+        cached = _FusedLayer(
+            qkv if qkv is not None else torch.cat((layer.q_proj, layer.k_proj, layer.v_proj)),
+            gate_up if gate_up is not None else torch.cat((layer.gate_proj, layer.up_proj)),
+        )
+        _fused_cache[layer] = cached
+    return cached
+
+
+def _layer_from_stacks(input_norm, qkv, o_proj, post_norm, gate_up, down_proj) -> LayerWeights:
+    intermediate = gate_up.shape[0] // 2
+    return LayerWeights(
+        input_norm=input_norm,
+        q_proj=qkv[:HIDDEN],
+        k_proj=qkv[HIDDEN : HIDDEN + KV_WIDTH],
+        v_proj=qkv[HIDDEN + KV_WIDTH :],
+        o_proj=o_proj,
+        post_attention_norm=post_norm,
+        gate_proj=gate_up[:intermediate],
+        up_proj=gate_up[intermediate:],
+        down_proj=down_proj,
+    )
+
+
+def random_weights(
+    *,
+    device: str | torch.device = "cuda:0",
+    seed: int = 0,
+    std: float = 0.02,
+    norm_std: float = 0.0,
+    layers: int = LAYERS,
+    vocab: int = VOCAB,
+    intermediate: int = INTERMEDIATE,
+) -> TinyLlamaWeights:
+    """Random-init fp16 TinyLlama-architecture weights: every projection, the embedding and
+    the LM head N(0, std); norm weights 1 + N(0, norm_std) (1 exactly by default, as a
+    freshly initialised Llama). Projections are allocated stacked (q|k|v, gate|up), so
+    the decoder's fused GEMMs use them without a copy."""
+    device = torch.device(device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+
+    def normal(*shape: int) -> Tensor:
+        return torch.empty(shape, dtype=torch.float16, device=device).normal_(0.0, std, generator=gen)
+
+    def norm() -> Tensor:
+        weight = torch.ones(HIDDEN, dtype=torch.float16, device=device)
+        if norm_std:
+            weight.add_(torch.empty_like(weight).normal_(0.0, norm_std, generator=gen))
+        return weight
+
+    built = []
+    for _ in range(layers):
+        built.append(
+            _layer_from_stacks(
+                norm(), normal(QKV_WIDTH, HIDDEN), normal(HIDDEN, HIDDEN), norm(), normal(2 * intermediate, HIDDEN),
+                normal(HIDDEN, intermediate),
+            )
+        )
+    return TinyLlamaWeights(normal(vocab, HIDDEN), tuple(built), norm(), normal(vocab, HIDDEN))
+
+
+def pack_weights(weights: TinyLlamaWeights) -> TinyLlamaWeights:
+    """A copy whose q/k/v and gate/up projections are stacked in memory (for weights loaded
+    as separate tensors), so decode runs its fused GEMMs without per-call concatenation."""
+    layers = []
+    for layer in weights.layers:
+        layers.append(
+            _layer_from_stacks(
+                layer.input_norm,
+                torch.cat((layer.q_proj, layer.k_proj, layer.v_proj)),
+                layer.o_proj,
+                layer.post_attention_norm,
+                torch.cat((layer.gate_proj, layer.up_proj)),
+                layer.down_proj,
+            )
+        )
+    return TinyLlamaWeights(weights.embedding, tuple(layers), weights.final_norm, weights.lm_head)
+
+
+# ---------------------------------------------------------------------------------------
+# RoPE table
+# ---------------------------------------------------------------------------------------
+
+_rope_tables: Dict[torch.device, Tensor] = {}
+
+
+def rope_table(device: torch.device) -> Tensor:
+    """FP16 [2048, 2, 32]: cos, then sin, of position * inv_freq[j] for every position.
+
+    Computed with the reference's own torch expressions (src/pagedcore/dense.py:47-54):
+    inv_freq = 1 / 10000^(arange(0, 64, 2) / 64) in fp32, angles = position * inv_freq in
+    fp32, cos/sin in fp32 rounded to fp16; the reference's cat((angles, angles)) repeats
+    the 32 values, so one copy per position is kept. The table is evaluated on the CPU and
+    copied to `device`: the GPU's fp32 pow gives inverse frequencies an ulp away from the
+    CPU's for some j, which the late positions (angles up to 2047 rad) amplify enough to
+    move fp16-rounded cos/sin entries; the CPU values are the ones the reference's CPU
+    tests pin.
+    """
+    device = torch.device(device)
+    table = _rope_tables.get(device)
+    if table is None:
+        with torch.autocast(device_type="cpu", enabled=False):
+            inverse = 1.0 / (ROPE_THETA ** (torch.arange(0, HEAD_DIM, 2).float() / HEAD_DIM))
+            angles = torch.arange(CONTEXT_LIMIT).float().unsqueeze(-1) * inverse
+            table = torch.stack((angles.cos().half(), angles.sin().half()), dim=1).contiguous().to(device)
+        _rope_tables[device] = table
+    return table
+
+
+# ---------------------------------------------------------------------------------------
+# Decode
+# ---------------------------------------------------------------------------------------
+
+
+def _check_weights(weights: TinyLlamaWeights, what: str) -> None:
+    if len(weights.layers) != LAYERS:
+        raise ValueError(f"paged {what} requires 22 decoder layers")
+
+
+def _check_gpu(allocator: KVAllocator, weights: TinyLlamaWeights, what: str) -> None:
+    """The kernels run on the GPU only: fail before any staging when the pool or the
+    weights live elsewhere (there is no CPU fallback)."""
+    if not allocator.pool.is_cuda or weights.embedding.device != allocator.pool.device:
+        raise RuntimeError(f"paged {what} runs on the GPU: the KV pool and the weights must share a CUDA device")
+
+
+@torch.inference_mode()
+def decode_paged(
+    input_ids: Tensor,
+    weights: TinyLlamaWeights,
+    allocator: KVAllocator,
+    request_ids: Tuple[RequestId, ...],
+) -> Tensor:
+    """One greedy-decode step for a batch: input_ids int64 [B, 1] (row b: the new token of
+    request_ids[b], at position = its cached length); returns fp16 logits [B, 1, vocab].
+
+    Each request gains one cached position on success; on any exception the staged step
+    is discarded and no request changes (reference src/pagedcore/decoder.py:156-199).
+    """
+    request_ids = tuple(request_ids)
+    if input_ids.dtype != torch.int64 or input_ids.ndim != 2 or input_ids.shape != (len(request_ids), 1):
+        raise ValueError("input_ids must be int64 [batch, 1] matching request IDs")
+    if input_ids.device != weights.embedding.device:
+        raise ValueError("input_ids and weights must be on the same device")
+    _check_weights(weights, "decode")
+    for request_id in request_ids:
+        allocator.cached_length(request_id)  # KeyError for an unknown request, as the reference
+    _check_gpu(allocator, weights, "decode")
+    with allocator.append_decode(request_ids):
+        table = rope_table(allocator.pool.device)
+        hidden = F.embedding(input_ids[:, 0], weights.embedding)  # [B, 2048]
+        x = torch.empty_like(hidden)
+        _hip.add_rms_norm(x, hidden, None, weights.layers[0].input_norm, RMS_EPS)
+        batch = len(request_ids)
+        for index, layer in enumerate(weights.layers):
+            fused = _fused(layer)
+            qkv = F.linear(x, fused.qkv)
+            query = allocator.write_decode_layers_rotary(request_ids, index, qkv, table)
+            attention = paged_attention_batch(query, allocator, request_ids, layer_index=index)
+            projected = F.linear(attention.view(batch, HIDDEN), layer.o_proj)
+            _hip.add_rms_norm(x, hidden, projected, layer.post_attention_norm, RMS_EPS)
+            gate_up = F.linear(x, fused.gate_up)
+            activated = torch.empty((batch, gate_up.shape[1] // 2), dtype=torch.float16, device=x.device)
+            _hip.silu_mul(activated, gate_up)
+            down = F.linear(activated, layer.down_proj)
+            following = weights.layers[index + 1].input_norm if index + 1 < LAYERS else weights.final_norm
+            _hip.add_rms_norm(x, hidden, down, following, RMS_EPS)
+        logits = F.linear(x, weights.lm_head)
+    return logits.unsqueeze(1)
+
+
+# ---------------------------------------------------------------------------------------
+# Prefill
+# ---------------------------------------------------------------------------------------
+
+
+def _dense_causal_attention(query: Tensor, key: Tensor, value: Tensor) -> Tensor:
+    """Prompt attention with the reference's fp16 rounding (src/pagedcore/dense.py:69-81):
+    fp16 scores scaled by 1/8, causal mask, fp32 softmax rounded to fp16, fp16 product.
+
+    query [T, 32, 64], key/value [T, 4, 64] (rotated K) -> [T, 2048]. The 8 query heads of
+    kv head g share it through a reshape instead of a repeat_interleave copy.
+    """
+    tokens = query.shape[0]
+    group = Q_HEADS // KV_HEADS
+    q = query.view(tokens, KV_HEADS, group, HEAD_DIM).permute(1, 2, 0, 3).reshape(KV_HEADS, group * tokens, HEAD_DIM)
+    k = key.permute(1, 2, 0).contiguous()  # [4, 64, T]
+    v = value.permute(1, 0, 2).contiguous()  # [4, T, 64]
+    scores = torch.matmul(q.contiguous(), k) * (HEAD_DIM**-0.5)  # [4, 8T, T] fp16
+    allowed = torch.ones((tokens, tokens), dtype=torch.bool, device=query.device).tril()
+    scores = scores.view(KV_HEADS, group, tokens, tokens).masked_fill(~allowed, torch.finfo(torch.float16).min)
+    probabilities = F.softmax(scores, dim=-1, dtype=torch.float32).to(torch.float16)
+    out = torch.matmul(probabilities.view(KV_HEADS, group * tokens, tokens), v)  # [4, 8T, 64]
+    return out.view(KV_HEADS, group, tokens, HEAD_DIM).permute(2, 0, 1, 3).reshape(tokens, HIDDEN)
+
+
+@torch.inference_mode()
+def prefill_paged(
+    input_ids: Tensor,
+    weights: TinyLlamaWeights,
+    allocator: KVAllocator,
+    request_id: RequestId,
+) -> Tensor:
+    """Prefill one admitted, empty request from int64 [1, T] prompt ids; returns fp16
+    logits [1, T, vocab]. Only K is rotated; the prompt's K/V are published through one
+    allocator.append after the forward succeeds (reference src/pagedcore/decoder.py:113-135).
+    """
+    if allocator.cached_length(request_id) != 0:
+        raise ValueError("paged prefill requires an empty request cache")
+    _check_weights(weights, "prefill")
+    if input_ids.dtype != torch.int64 or input_ids.ndim != 2 or input_ids.shape[0] != 1:
+        raise ValueError("input_ids must be int64 [1, tokens]")
+    if input_ids.device != weights.embedding.device:
+        raise ValueError("input_ids and weights must be on the same device")
+    tokens = input_ids.shape[1]
+    if tokens < 1 or tokens > CONTEXT_LIMIT:
+        raise ValueError("forward requires 1 to 2048 total cached token positions")
+    _check_gpu(allocator, weights, "prefill")
+    device = input_ids.device
+    table = rope_table(device)
+    positions = torch.arange(tokens, dtype=torch.int64, device=device)
+    hidden = F.embedding(input_ids[0], weights.embedding)  # [T, 2048]
+    x = torch.empty_like(hidden)
+    _hip.add_rms_norm(x, hidden, None, weights.layers[0].input_norm, RMS_EPS)
+    keys = torch.empty((LAYERS, tokens, KV_HEADS, HEAD_DIM), dtype=torch.float16, device=device)
+    values = torch.empty_like(keys)
+    query = torch.empty((tokens, Q_HEADS, HEAD_DIM), dtype=torch.float16, device=device)
+    for index, layer in enumerate(weights.layers):
+        fused = _fused(layer)
+        qkv = F.linear(x, fused.qkv)
+        _hip.rope_kv_append(query, qkv, positions, table, key_out=keys[index], value_out=values[index])
+        attention = _dense_causal_attention(query, keys[index], values[index])
+        projected = F.linear(attention, layer.o_proj)
+        _hip.add_rms_norm(x, hidden, projected, layer.post_attention_norm, RMS_EPS)
+        gate_up = F.linear(x, fused.gate_up)
+        activated = torch.empty((tokens, gate_up.shape[1] // 2), dtype=torch.float16, device=device)
+        _hip.silu_mul(activated, gate_up)
+        down = F.linear(activated, layer.down_proj)
+        following = weights.layers[index + 1].input_norm if index + 1 < LAYERS else weights.final_norm
+        _hip.add_rms_norm(x, hidden, down, following, RMS_EPS)
+    logits = F.linear(x, weights.lm_head)
+    allocator.append(request_id, keys, values)
+    return logits.unsqueeze(0)

@@ -38,6 +38,7 @@ BLOCK_TOKENS = 16
 KV_HEADS = 4
 HEAD_DIM = 64
 CONTEXT_LIMIT = 2048
+QKV_COLUMNS = (32 + 2 * KV_HEADS) * HEAD_DIM  # 2560: one token's q | k | v projections
 MAX_BLOCKS_PER_REQUEST = CONTEXT_LIMIT // BLOCK_TOKENS  # 128
 
 
@@ -80,6 +81,14 @@ class KVWriter(Protocol):
         self, pool: Tensor, layer_begin: int, key: Tensor, value: Tensor, slots: Sequence[int]
     ) -> None: ...
 
+    def rope_append(
+        self, pool: Tensor, layer: int, qkv: Tensor, rope_table: Tensor, positions: Tensor, slots: Tensor,
+        query_out: Tensor,
+    ) -> None:
+        """RoPE on each row's query and key at `positions`; rotated key and value to
+        pool[layer, 0/1, slot // 16, slot % 16]; rotated queries to query_out [B, 32, 1, 64]."""
+        ...
+
 
 class HipKVWriter:
     """The GPU data path: one `pc_kv_append` launch per call, on the current stream."""
@@ -96,11 +105,22 @@ class HipKVWriter:
             slot_mapping = torch.as_tensor(np.asarray(slots, dtype=np.int64)).to(pool.device)
         _hip.kv_append(pool, layer_begin, key, value, slot_mapping)
 
+    def rope_append(
+        self, pool: Tensor, layer: int, qkv: Tensor, rope_table: Tensor, positions: Tensor, slots: Tensor,
+        query_out: Tensor,
+    ) -> None:
+        _hip.rope_kv_append(query_out, qkv, positions, rope_table, pool=pool, layer=layer, slot_mapping=slots)
+
 
 class _HostOnlyWriter:
     """Stand-in for CPU pools: bookkeeping works, moving KV bytes does not."""
 
     def append(self, pool: Tensor, layer_begin: int, key: Tensor, value: Tensor, slots: Sequence[int]) -> None:
+        raise RuntimeError(
+            "KV writes run on the GPU: this allocator's pool is on the CPU and has no KV writer"
+        )
+
+    def rope_append(self, *args) -> None:
         raise RuntimeError(
             "KV writes run on the GPU: this allocator's pool is on the CPU and has no KV writer"
         )
@@ -129,6 +149,41 @@ class _SequenceCache:
 class _TokenAppend:
     sequence: _SequenceCache
     written_layers: int = 0
+
+
+def _counting(base: type, names: Tuple[str, ...]) -> type:
+    """Subclass of list/dict whose mutating methods bump a `mutations` counter, so the
+    accounting check can tell in O(1) whether a container changed since it was verified."""
+
+    def wrap(name: str):
+        method = getattr(base, name)
+
+        def counted(self, *args, **kwargs):
+            self.mutations += 1
+            return method(self, *args, **kwargs)
+
+        counted.__name__ = name
+        return counted
+
+    namespace = {name: wrap(name) for name in names}
+    namespace["__slots__"] = ("mutations",)
+
+    def __init__(self, *args, **kwargs):
+        base.__init__(self, *args, **kwargs)
+        self.mutations = 0
+
+    namespace["__init__"] = __init__
+    return type(f"_Counting{base.__name__.title()}", (base,), namespace)
+
+
+_CountingList = _counting(
+    list,
+    ("__setitem__", "__delitem__", "__iadd__", "__imul__", "append", "extend", "insert", "pop", "remove",
+     "clear", "sort", "reverse"),
+)
+_CountingDict = _counting(
+    dict, ("__setitem__", "__delitem__", "__ior__", "pop", "popitem", "clear", "update", "setdefault")
+)
 
 
 def _slot_mapping(blocks: BlockTable, start: int, count: int) -> np.ndarray:
@@ -164,15 +219,17 @@ class KVAllocator:
         self._writer = kv_writer
         self._worker = current_thread()
         self._stream = torch.cuda.current_stream(pool.device) if pool.is_cuda else None
-        self._free_blocks = [BlockId(index) for index in reversed(range(pool.shape[2]))]
-        self._sequences: Dict[RequestId, _SequenceCache] = {}
+        self._free_blocks = _CountingList(BlockId(index) for index in reversed(range(pool.shape[2])))
+        self._sequences: Dict[RequestId, _SequenceCache] = _CountingDict()
         # Tables are checked against the owners recorded when blocks are assigned.
-        self._block_owners: Dict[BlockId, RequestId] = {}
+        self._block_owners: Dict[BlockId, RequestId] = _CountingDict()
+        # (container identities and mutation counts, counts) of the last verified state.
+        self._verified: Optional[Tuple[tuple, CapacityCounts]] = None
         self._decode_appends: Optional[Dict[RequestId, _TokenAppend]] = None
         # Bumped whenever a table or length may change; keys the device-table cache.
         self._version = 0
         self._table_cache: Dict[tuple, _DecodeBatch] = {}
-        self._decode_slot_cache: Dict[Tuple[RequestId, ...], Tensor] = {}
+        self._decode_slot_cache: Dict[Tuple[RequestId, ...], Tuple[Tensor, Tensor]] = {}
 
     @property
     def pool(self) -> Tensor:
@@ -291,6 +348,7 @@ class KVAllocator:
             yield
             if any(append.written_layers != LAYERS for append in appends.values()):
                 raise RuntimeError("decode must write every cache layer before committing")
+            before = self._verified_counts()
             if additional:
                 del self._free_blocks[-additional:]
             for request_id, append in appends.items():
@@ -298,7 +356,24 @@ class KVAllocator:
                 for block in append.sequence.blocks[len(original.blocks) :]:
                     self._block_owners[block] = request_id
                 self._sequences[request_id] = append.sequence
-            self._assert_accounting()
+            if before is None:
+                self._assert_accounting()
+            else:
+                # The state was verified when the step began and nothing changed it since:
+                # the commit only moves `additional` verified free blocks (distinct, in
+                # range, unowned) to the requests that staged them and lengthens each
+                # staged request by one position within its credits (checked at staging),
+                # so every invariant still holds and the counts move by exactly that.
+                self._remember(
+                    CapacityCounts(
+                        total_blocks=before.total_blocks,
+                        free_blocks=before.free_blocks - additional,
+                        owned_blocks=before.owned_blocks + additional,
+                        reserved_blocks=before.reserved_blocks,
+                        active_slots=before.active_slots,
+                        live_cached_token_slots=before.live_cached_token_slots + len(appends),
+                    )
+                )
         finally:
             self._decode_appends = None
             self._touch()
@@ -309,7 +384,7 @@ class KVAllocator:
     ) -> None:
         """Write one token's rotated K / unrotated V, FP16 [4, 64], in layer order."""
         self._check_worker()
-        self._assert_accounting()
+        self._check_staged_state()
         if self._decode_appends is None:
             raise RuntimeError("decode writes require a staged append")
         append = self._decode_appends[request_id]
@@ -342,7 +417,7 @@ class KVAllocator:
         Every row is checked before the single launch; written layers advance together.
         """
         self._check_worker()
-        self._assert_accounting()
+        self._check_staged_state()
         if self._decode_appends is None:
             raise RuntimeError("decode writes require a staged append")
         if not request_ids or len(set(request_ids)) != len(request_ids):
@@ -359,25 +434,85 @@ class KVAllocator:
             for tensor in (key, value)
         ):
             raise ValueError("K and V must share FP16 [batch, 4, 64] on the pool device")
-        slots = self._decode_slots(request_ids, appends)
+        slots, _ = self._decode_slots(request_ids, appends)
         self._writer.append(self._pool, layer_index, key[None], value[None], slots)
         for append in appends:
             append.written_layers += 1
 
+    @torch.inference_mode()
+    def write_decode_layers_rotary(
+        self,
+        request_ids: Tuple[RequestId, ...],
+        layer_index: int,
+        qkv: Tensor,
+        rope_table: Tensor,
+    ) -> Tensor:
+        """Fused RoPE + write_decode_layers, the batched decoder's per-layer write.
+
+        qkv: FP16 [B, >= 2560] on the pool device, unit column stride: row b holds the
+        query (32 x 64), key (4 x 64) and value (4 x 64) projections of request_ids[b]'s
+        new token. rope_table: FP16 [rope positions, 2, 32] cos/sin table. Row b's query and
+        key are rotated at the request's position (its cached length before this step, as
+        the reference decoder passes it to apply_rope, src/pagedcore/decoder.py:173-186);
+        the rotated key and the unrotated value go to the staged slot of this layer, like
+        write_decode_layer. Returns the rotated queries, FP16 [B, 32, 1, 64]. Same checks,
+        errors and layer-order rules as write_decode_layers; one launch for all rows.
+        """
+        self._check_worker()
+        self._check_staged_state()
+        if self._decode_appends is None:
+            raise RuntimeError("decode writes require a staged append")
+        if not request_ids or len(set(request_ids)) != len(request_ids):
+            raise ValueError("decode requires nonempty, distinct request IDs")
+        appends = [self._decode_appends[request_id] for request_id in request_ids]
+        if type(layer_index) is not int or not 0 <= layer_index < LAYERS:
+            raise ValueError("layer_index must identify one of the 22 decoder layers")
+        if any(layer_index != append.written_layers for append in appends):
+            raise ValueError("decode cache layers must be written once in order")
+        if (
+            qkv.ndim != 2
+            or qkv.shape[0] != len(request_ids)
+            or qkv.shape[1] < QKV_COLUMNS
+            or qkv.stride(1) != 1
+            or qkv.dtype != torch.float16
+            or qkv.device != self._pool.device
+        ):
+            raise ValueError("qkv must be FP16 [batch, >= 2560] rows on the pool device")
+        if (
+            rope_table.ndim != 3
+            or rope_table.shape[1:] != (2, HEAD_DIM // 2)
+            or rope_table.shape[0] < CONTEXT_LIMIT
+            or rope_table.dtype != torch.float16
+            or rope_table.device != self._pool.device
+            or not rope_table.is_contiguous()
+        ):
+            raise ValueError("rope_table must be contiguous FP16 [>= 2048, 2, 32] on the pool device")
+        slots, positions = self._decode_slots(request_ids, appends)
+        query = torch.empty((len(request_ids), 32, 1, HEAD_DIM), dtype=torch.float16, device=self._pool.device)
+        self._writer.rope_append(self._pool, layer_index, qkv, rope_table, positions, slots, query)
+        for append in appends:
+            append.written_layers += 1
+        return query
+
     def _decode_slots(self, request_ids: Tuple[RequestId, ...], appends: Sequence[_TokenAppend]):
-        """Slot of each staged token; a device tensor cached for the decode step on GPU pools."""
+        """(slot, position) of each staged token: slot = block * 16 + offset of position
+        length - 1; device int64 tensors cached for the decode step on GPU pools."""
         cached = self._decode_slot_cache.get(request_ids)
         if cached is not None:
             return cached
         slots = np.empty(len(appends), dtype=np.int64)
+        positions = np.empty(len(appends), dtype=np.int64)
         for row, append in enumerate(appends):
-            logical_block, slot = divmod(append.sequence.length - 1, BLOCK_TOKENS)
+            position = append.sequence.length - 1
+            logical_block, slot = divmod(position, BLOCK_TOKENS)
             slots[row] = append.sequence.blocks[logical_block] * BLOCK_TOKENS + slot
+            positions[row] = position
         if not self._pool.is_cuda:
-            return slots
-        device_slots = torch.from_numpy(slots).to(self._pool.device)
-        self._decode_slot_cache[request_ids] = device_slots
-        return device_slots
+            return slots, positions
+        both = torch.from_numpy(np.stack([slots, positions])).to(self._pool.device)
+        result = (both[0], both[1])
+        self._decode_slot_cache[request_ids] = result
+        return result
 
     def iter_layer_blocks(
         self, request_id: RequestId, *, layer_index: int
@@ -400,7 +535,7 @@ class KVAllocator:
         request (KeyError), unwritten staged layer (RuntimeError), empty cache (ValueError).
         """
         self._check_worker()
-        self._assert_accounting()
+        self._check_staged_state((request_id,))
         if type(layer_index) is not int or not 0 <= layer_index < LAYERS:
             raise ValueError("layer_index must identify one of the 22 decoder layers")
         return self._staged_sequence(request_id, layer_index)
@@ -442,7 +577,7 @@ class KVAllocator:
         if not request_ids:
             raise ValueError("attention requires at least one request")
         self._check_worker()
-        self._assert_accounting()
+        self._check_staged_state(request_ids)
         if type(layer_index) is not int or not 0 <= layer_index < LAYERS:
             raise ValueError("layer_index must identify one of the 22 decoder layers")
         sequences = [self._staged_sequence(request_id, layer_index) for request_id in request_ids]
@@ -498,6 +633,21 @@ class KVAllocator:
         self._table_cache.clear()
         self._decode_slot_cache.clear()
 
+    def _check_staged_state(self, request_ids: Optional[Sequence[RequestId]] = None) -> None:
+        """Accounting check of the per-layer calls of a decode step.
+
+        Outside a staged decode this is the full _assert_accounting. Inside one, every
+        mutation through this API raises, the staged tables and lengths of the step's
+        requests are private copies verified by the full check when the step began, and
+        the commit runs the full check again before anything is published; so calls that
+        only touch the step's requests (request_ids None: the write calls, which look the
+        requests up in the staged set) skip the O(pool) scan, which would otherwise run
+        twice per layer.
+        """
+        appends = self._decode_appends
+        if appends is None or (request_ids is not None and any(r not in appends for r in request_ids)):
+            self._assert_accounting()
+
     def _check_mutation(self) -> None:
         self._check_worker()
         if self._decode_appends is not None:
@@ -509,12 +659,43 @@ class KVAllocator:
         if self._stream is not None and torch.cuda.current_stream(self._pool.device) != self._stream:
             raise RuntimeError("KV allocator must use its owning CUDA stream")
 
+    def _state_key(self) -> Optional[tuple]:
+        """Identity and mutation count of each bookkeeping container (None if one of them
+        is not a counting container, e.g. replaced from outside: then nothing is cached)."""
+        containers = (self._free_blocks, self._sequences, self._block_owners)
+        if not all(isinstance(c, (_CountingList, _CountingDict)) for c in containers):
+            return None
+        return tuple((id(c), c.mutations) for c in containers)
+
+    def _verified_counts(self) -> Optional[CapacityCounts]:
+        """The counts of the last full check if no container changed since, else None."""
+        key = self._state_key()
+        if key is not None and self._verified is not None and self._verified[0] == key:
+            return self._verified[1]
+        return None
+
+    def _remember(self, counts: CapacityCounts) -> None:
+        key = self._state_key()
+        self._verified = None if key is None else (key, counts)
+
     def _assert_accounting(self) -> CapacityCounts:
         """Full ownership invariants (reference src/pagedcore/kv_cache.py:314-357).
 
-        Same checks and messages; the per-block type/range scans run as C-level set and
-        min/max passes rather than a Python loop.
+        Same checks and messages. The check is a pure function of the three bookkeeping
+        containers, which count their own mutations: when none changed since the last
+        full check passed, its counts are returned without rescanning the pool (any
+        change, including one made from outside through the containers' methods, forces
+        the full scan). The per-block type/range scans run as C-level set and min/max
+        passes rather than a Python loop.
         """
+        cached = self._verified_counts()
+        if cached is not None:
+            return cached
+        counts = self._full_accounting()
+        self._remember(counts)
+        return counts
+
+    def _full_accounting(self) -> CapacityCounts:
         total = self._pool.shape[2]
         for request_id, sequence in self._sequences.items():
             if (

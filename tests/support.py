@@ -34,6 +34,9 @@ class CpuCopyWriter:
         pool[layers, 0, blocks, offsets] = key
         pool[layers, 1, blocks, offsets] = value
 
+    def rope_append(self, *args) -> None:
+        raise RuntimeError("the CPU test writer does not rotate")
+
 
 def cpu_allocator(pool: Tensor, writer: Optional[CpuCopyWriter] = None) -> KVAllocator:
     return KVAllocator(pool, kv_writer=writer if writer is not None else CpuCopyWriter())

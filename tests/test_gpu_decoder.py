@@ -1,0 +1,382 @@
+"""The batched decode step on the GPU: its three elementwise kernels against the oracle's
+torch expressions, then decode_paged / prefill_paged against the contiguous CPU forward
+(the reference's own expectation, tests/unit/test_decoder.py:114-195: logits within 5e-3,
+cached K/V within 2e-3, old slots bit-identical)."""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import decoder_reference as dref
+from pagedcore_amd import _hip
+from pagedcore_amd import decoder as dec
+from pagedcore_amd.engine_types import CapacityCounts, KVReservation, RequestId
+from pagedcore_amd.kv_cache import KVAllocator
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(tensor: torch.Tensor) -> np.ndarray:
+    return tensor.detach().cpu().contiguous().view(torch.int16).numpy()
+
+
+def _ulps(got: torch.Tensor, expected: torch.Tensor) -> int:
+    """Largest distance in fp16 units in the last place (same-sign values)."""
+    a = _bits(got).astype(np.int32)
+    b = _bits(expected).astype(np.int32)
+    a = np.where(a < 0, -(a & 0x7FFF), a)
+    b = np.where(b < 0, -(b & 0x7FFF), b)
+    return int(np.abs(a - b).max()) if a.size else 0
+
+
+# ---------------------------------------------------------------------------------------
+# Kernels
+# ---------------------------------------------------------------------------------------
+
+
+def test_rope_table_matches_the_oracle(device):
+    table = dec.rope_table(device).cpu()
+    assert table.shape == (2048, 2, 32) and table.dtype == torch.float16
+    cosine, sine = dref.rope_cos_sin(torch.arange(2048)[None], torch.float16)
+    assert torch.equal(table[:, 0], cosine[0, 0, :, :32]) and torch.equal(table[:, 1], sine[0, 0, :, :32])
+    assert torch.equal(cosine[0, 0, :, :32], cosine[0, 0, :, 32:])
+
+
+@pytest.mark.parametrize("tokens,stride", [(1, 2560), (7, 2560), (300, 2568)])
+def test_rope_kv_append_is_bit_exact(device, tokens, stride):
+    """Rotated q/k equal the reference rotation (dense.py:56-59) evaluated by torch with the
+    same fp16 cos/sin values, bit for bit; K and V land in their slots and nothing else in
+    the pool changes."""
+    gen = torch.Generator(device=device).manual_seed(tokens)
+    qkv = torch.randn(tokens, stride, dtype=torch.float16, device=device, generator=gen)
+    positions = torch.randint(0, 2048, (tokens,), device=device, generator=gen)
+    positions[0] = 0
+    if tokens > 1:
+        positions[1] = 2047
+    blocks = 40
+    pool = torch.full((22, 2, blocks, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    slots = torch.randperm(blocks * 16, device=device, generator=gen)[:tokens]
+    if tokens > 2:
+        slots[2] = -1  # skipped token
+    table = dec.rope_table(device)
+    query = torch.empty(tokens, 32, 64, dtype=torch.float16, device=device)
+    keys = torch.empty(tokens, 4, 64, dtype=torch.float16, device=device)
+    values = torch.empty_like(keys)
+    _hip.rope_kv_append(query, qkv, positions, table, key_out=keys, value_out=values, pool=pool, layer=5,
+                        slot_mapping=slots)
+    torch.cuda.synchronize()
+
+    host = qkv.cpu()
+    t = table.cpu()[positions.cpu()]  # [tokens, 2, 32]
+    cosine = torch.cat((t[:, 0], t[:, 0]), dim=-1)[:, None, :]
+    sine = torch.cat((t[:, 1], t[:, 1]), dim=-1)[:, None, :]
+    expected_q = dref.rotate(host[:, :2048].reshape(tokens, 32, 64), cosine, sine)
+    expected_k = dref.rotate(host[:, 2048:2304].reshape(tokens, 4, 64), cosine, sine)
+    expected_v = host[:, 2304:2560].reshape(tokens, 4, 64)
+    assert np.array_equal(_bits(query), _bits(expected_q))
+    assert np.array_equal(_bits(keys), _bits(expected_k))
+    assert np.array_equal(_bits(values), _bits(expected_v))
+
+    host_pool = pool.cpu()
+    written = torch.zeros(22, 2, blocks * 16, dtype=torch.bool)
+    for token, slot in enumerate(slots.cpu().tolist()):
+        if slot < 0:
+            continue
+        block, offset = divmod(slot, 16)
+        assert np.array_equal(_bits(host_pool[5, 0, block, offset]), _bits(expected_k[token]))
+        assert np.array_equal(_bits(host_pool[5, 1, block, offset]), _bits(expected_v[token]))
+        written[5, :, slot] = True
+    untouched = host_pool.view(22, 2, blocks * 16, 256)[~written]
+    assert torch.isnan(untouched).all()
+
+
+def test_rope_kv_append_rejects_bad_arguments_without_a_gpu_launch(device):
+    lib = _hip.load()
+    q = torch.empty(2, 32, 64, dtype=torch.float16, device=device)
+    qkv = torch.empty(2, 2560, dtype=torch.float16, device=device)
+    pos = torch.zeros(2, dtype=torch.int64, device=device)
+    table = dec.rope_table(device)
+    call = lambda **kw: lib.pc_rope_kv_append(  # noqa: E731
+        kw.get("q", q.data_ptr()), None, None, qkv.data_ptr(), kw.get("stride", 2560), pos.data_ptr(),
+        table.data_ptr(), 2048, kw.get("pool"), 4, kw.get("layer", 0), kw.get("slots"), 2, None,
+    )
+    assert call(stride=2552) == 1 and b"qkv_stride" in lib.pc_last_error()
+    assert call(q=q.data_ptr() + 2) == 1 and b"aligned" in lib.pc_last_error()
+    assert call(pool=q.data_ptr()) == 1 and b"both" in lib.pc_last_error()
+    assert call(pool=q.data_ptr(), slots=pos.data_ptr(), layer=22) == 1 and b"layer" in lib.pc_last_error()
+
+
+@pytest.mark.parametrize("rows,width,with_delta", [(1, 2048, False), (7, 2048, True), (3, 8192, True), (5, 520, True), (0, 2048, True)])
+def test_add_rms_norm_matches_the_oracle(device, rows, width, with_delta):
+    gen = torch.Generator(device=device).manual_seed(rows * 1000 + width)
+    hidden = (torch.randn(rows, width, device=device, generator=gen) * 3).half()
+    delta = torch.randn(rows, width, device=device, generator=gen).half() if with_delta else None
+    weight = (1 + 0.2 * torch.randn(width, device=device, generator=gen)).half()
+    out = torch.empty_like(hidden)
+    expected_hidden = hidden.cpu() + delta.cpu() if with_delta else hidden.cpu()
+    _hip.add_rms_norm(out, hidden, delta, weight)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(hidden), _bits(expected_hidden))  # fp16 residual sum, in place
+    expected = dref.rms_norm(expected_hidden, weight.cpu())
+    assert _ulps(out, expected) <= 1  # only the fp32 sum order differs
+
+
+def test_silu_mul_matches_torch(device):
+    gen = torch.Generator(device=device).manual_seed(9)
+    gate_up = (torch.randn(9, 2 * 5632, device=device, generator=gen) * 4).half()
+    out = torch.empty(9, 5632, dtype=torch.float16, device=device)
+    _hip.silu_mul(out, gate_up)
+    torch.cuda.synchronize()
+    host = gate_up.cpu()
+    expected = F.silu(host[:, :5632]) * host[:, 5632:]
+    assert _ulps(out, expected) <= 1
+
+
+# ---------------------------------------------------------------------------------------
+# Decode step and prefill
+#
+# Error model. The reference's decoder tolerances (logits 5e-3, K/V 2e-3) compare two paths
+# that run the same GEMMs on the same device. Here the expectation is the CPU forward, whose
+# fp16 GEMM outputs round differently from hipBLASLt's (fp32 sums in another order); through
+# 22 layers that noise reaches the reference's tolerances. So the tests (1) hold the decode
+# step to 5e-3 / 2e-3 with the oracle started from the GPU's own cache, as in the
+# reference's test, where prefill is exact; (2) hold layer 0 of prefill (no attention noise
+# upstream) to 2e-3; and (3) everywhere else require the GPU to be as close to an fp32
+# evaluation of the same weights as the reference's own fp16 computation is:
+#     max|gpu - fp32| <= 1.25 * max|cpu fp16 - fp32| + 2e-3.
+# A real defect (wrong position, norm, head map or slot) misses every one of these by far.
+# ---------------------------------------------------------------------------------------
+
+
+def _synthetic(device):
+    """The reference test's synthetic geometry: hidden 2048, 32/4 heads, MLP 32, vocab 31,
+    two distinct layers repeated 11 times to fill the pool's 22 layers."""
+    small = dec.random_weights(device=device, seed=11, layers=2, vocab=31, intermediate=32, norm_std=0.1)
+    return dec.TinyLlamaWeights(small.embedding, small.layers * 11, small.final_norm, small.lm_head)
+
+
+def _cpu(weights):
+    return dref.to_cpu(weights, dec.LayerWeights, dec.TinyLlamaWeights)
+
+
+def _fp32(host_weights):
+    layers = tuple(
+        SimpleNamespace(**{name: getattr(layer, name).float() for name in dref._LAYER_FIELDS}) for layer in host_weights.layers
+    )
+    return SimpleNamespace(
+        embedding=host_weights.embedding.float(), layers=layers, final_norm=host_weights.final_norm.float(),
+        lm_head=host_weights.lm_head.float(),
+    )
+
+
+def _gap(a, b) -> float:
+    return (a.float().cpu() - b.float().cpu()).abs().max().item()
+
+
+def _as_accurate(gpu, cpu16, fp32) -> None:
+    assert _gap(gpu, fp32) <= 1.25 * _gap(cpu16, fp32) + 2e-3, (_gap(gpu, fp32), _gap(cpu16, fp32))
+
+
+def _pool_cache(allocator, request):
+    """The request's cached K/V as the contiguous forward holds them: per layer
+    ([1, 4, length, 64], [1, 4, length, 64]) on the CPU."""
+    length = allocator.cached_length(request)
+    layers = []
+    for layer in range(22):
+        pair = []
+        for kind in range(2):
+            rows = torch.cat([allocator.pool[layer, kind, block] for block in allocator.block_table(request)])[:length]
+            pair.append(rows.cpu().transpose(0, 1)[None])
+        layers.append(tuple(pair))
+    return layers
+
+
+@pytest.mark.parametrize("lengths", [(1, 15, 16, 17, 49)])
+def test_prefill_paged_matches_the_contiguous_prefill(device, lengths):
+    weights = _synthetic(device)
+    host_weights = _cpu(weights)
+    exact = _fp32(host_weights)
+    pool = torch.full((22, 2, 16, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    for row, length in enumerate(lengths):
+        request = RequestId(str(row))
+        allocator.create(KVReservation(request, (length + 15) // 16))
+        ids = (torch.arange(length)[None] + length) % 31
+        expected_logits, cache = dref.prefill(ids, host_weights)
+        exact_logits, exact_cache = dref.forward(ids, exact)
+        before = pool.cpu()
+        logits = dec.prefill_paged(ids.to(device), weights, allocator, request)
+        assert logits.shape == (1, length, 31) and logits.dtype == torch.float16
+        torch.testing.assert_close(logits.cpu(), expected_logits, atol=5e-3, rtol=5e-3)
+        _as_accurate(logits, expected_logits, exact_logits)
+        assert allocator.cached_length(request) == length
+        got = _pool_cache(allocator, request)
+        for layer in range(22):
+            for kind in range(2):
+                if layer == 0:
+                    torch.testing.assert_close(got[0][kind], cache[0][kind], atol=2e-3, rtol=2e-3)
+                _as_accurate(got[layer][kind], cache[layer][kind], exact_cache[layer][kind])
+        # slots past the prompt and blocks of no request keep their poison
+        after = pool.cpu()
+        table = allocator.block_table(request)
+        tail = length - (len(table) - 1) * 16
+        assert torch.isnan(after[:, :, table[-1], tail:]).all()
+        others = [b for b in range(16) if b not in table]
+        assert torch.equal(after[:, :, others].isnan(), before[:, :, others].isnan())
+
+
+@pytest.mark.parametrize("lengths", [(15,), (1, 15, 16, 17, 49)])
+def test_decode_paged_matches_the_contiguous_fp32_decode(device, lengths):
+    """tests/unit/test_decoder.py:114-195: two steps (the second in reverse request order);
+    per row the logits within 5e-3 and the new K/V within 2e-3 of decode(fp32_attention=True)
+    started from the same cache; old slots bit-identical; accounting as the reference."""
+    weights = _synthetic(device)
+    host_weights = _cpu(weights)
+    pool = torch.full((22, 2, 16, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    requests = tuple(RequestId(str(row)) for row in range(len(lengths)))
+    for request, length in zip(requests, lengths):
+        allocator.create(KVReservation(request, (length + 2 + 15) // 16))
+        dec.prefill_paged(((torch.arange(length)[None] + length) % 31).to(device), weights, allocator, request)
+    pointer = pool.untyped_storage().data_ptr()
+    counts = allocator.capacity()
+    for step in range(2):
+        order = requests if step == 0 else requests[::-1]
+        tokens = torch.tensor([[2 + step + int(request)] for request in order])
+        caches = {request: _pool_cache(allocator, request) for request in order}
+        expected = [dref.decode_fp32(tokens[row : row + 1], caches[request], host_weights) for row, request in enumerate(order)]
+        before = pool.cpu()
+        logits = dec.decode_paged(tokens.to(device), weights, allocator, order)
+        torch.cuda.synchronize()
+        assert logits.shape == (len(order), 1, 31) and logits.dtype == torch.float16
+        assert torch.isfinite(logits).all()
+        for row, request in enumerate(order):
+            expected_logits, cache = expected[row]
+            old_length = caches[request][0][0].shape[2]
+            torch.testing.assert_close(logits[row : row + 1].cpu(), expected_logits, atol=5e-3, rtol=5e-3)
+            assert allocator.cached_length(request) == old_length + 1
+            got = _pool_cache(allocator, request)
+            for layer in range(22):
+                for kind in range(2):
+                    # old positions untouched, the new one within 2e-3
+                    assert torch.equal(got[layer][kind][:, :, :old_length], caches[request][layer][kind])
+                    torch.testing.assert_close(
+                        got[layer][kind][:, :, old_length], cache[layer][kind][:, :, old_length], atol=2e-3, rtol=2e-3
+                    )
+            table = allocator.block_table(request)
+            block, slot = divmod(old_length, 16)
+            after = pool.cpu()
+            # the rest of the new token's block is still the poison it held before
+            assert torch.equal(after[:, :, table[block], slot + 1 :].isnan(), before[:, :, table[block], slot + 1 :].isnan())
+        current = allocator.capacity()
+        assert current.live_cached_token_slots == sum(lengths) + len(order) * (step + 1)
+        assert current.reserved_blocks == counts.reserved_blocks
+        assert current.active_slots == len(order)
+        assert pool.untyped_storage().data_ptr() == pointer
+    for request in requests:
+        allocator.release_all(request)
+    assert allocator.capacity() == CapacityCounts(16, 16, 0, 0, 0, 0)
+
+
+def test_full_size_decode_is_as_accurate_as_the_reference_computation(device):
+    """22 distinct full-size layers (MLP 5632, vocab 32000, random N(0, 0.02) weights, norm
+    weights 1 + N(0, 0.1)): prefill and decode logits are as close to the fp32 evaluation
+    as the CPU fp16 forward is, and the greedy token agrees wherever the fp32 top-2 margin
+    exceeds that noise."""
+    weights = dec.random_weights(device=device, seed=5, norm_std=0.1)
+    host_weights = _cpu(weights)
+    exact = _fp32(host_weights)
+    lengths = (3, 17, 40)
+    pool = torch.full((22, 2, 12, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    requests = tuple(RequestId(f"full{row}") for row in range(len(lengths)))
+    gen = torch.Generator().manual_seed(2)
+    for request, length in zip(requests, lengths):
+        allocator.create(KVReservation(request, (length + 1 + 15) // 16))
+        ids = torch.randint(0, 32000, (1, length), generator=gen)
+        logits = dec.prefill_paged(ids.to(device), weights, allocator, request)
+        _as_accurate(logits, dref.prefill(ids, host_weights)[0], dref.forward(ids, exact)[0])
+    tokens = torch.randint(0, 32000, (len(lengths), 1), generator=gen)
+    caches = {request: _pool_cache(allocator, request) for request in requests}
+    logits = dec.decode_paged(tokens.to(device), weights, allocator, requests)
+    for row, request in enumerate(requests):
+        cpu16 = dref.decode_fp32(tokens[row : row + 1], caches[request], host_weights)[0]
+        fp32 = dref.forward(tokens[row : row + 1], exact, [(k.float(), v.float()) for k, v in caches[request]], fp32_attention=True)[0]
+        _as_accurate(logits[row : row + 1], cpu16, fp32)
+        top = fp32.flatten().topk(2).values
+        if float(top[0] - top[1]) > 4 * _gap(cpu16, fp32):
+            assert int(logits[row].argmax()) == int(fp32.argmax())
+
+
+def test_decode_paged_rows_do_not_depend_on_batch_composition(device):
+    """tests/unit/test_decoder.py:198-239: decoding requests together or one at a time gives
+    bit-identical logits and cached K/V (the GEMM kernels chosen for these row counts sum
+    each output in the same order)."""
+    weights = _synthetic(device)
+    requests = tuple(RequestId(str(row)) for row in range(3))
+    pools = [torch.full((22, 2, 12, 16, 4, 64), float("nan"), dtype=torch.float16, device=device) for _ in range(2)]
+    separate, batched = (KVAllocator(pool) for pool in pools)
+    for request, length in zip(requests, (1, 16, 49)):
+        ids = (torch.arange(length)[None] % 31).to(device)
+        for allocator in (separate, batched):
+            allocator.create(KVReservation(request, (length + 18) // 16))
+            dec.prefill_paged(ids, weights, allocator, request)
+    for step in range(3):
+        order = requests if step % 2 == 0 else requests[::-1]
+        tokens = torch.tensor([[3 + int(request) + step] for request in order], device=device)
+        expected = torch.cat([dec.decode_paged(tokens[row : row + 1], weights, separate, (request,)) for row, request in enumerate(order)])
+        actual = dec.decode_paged(tokens, weights, batched, order)
+        torch.testing.assert_close(actual, expected, atol=0, rtol=0)
+        assert torch.equal(actual.argmax(-1), expected.argmax(-1))
+        assert batched.capacity() == separate.capacity()
+        for request in order:
+            assert batched.cached_length(request) == separate.cached_length(request)
+            for block in range(len(batched.block_table(request))):
+                for actual_kv, expected_kv in zip(batched.read_block(request, block), separate.read_block(request, block)):
+                    torch.testing.assert_close(actual_kv, expected_kv, atol=0, rtol=0)
+
+
+def test_decode_paged_failure_discards_the_step(device, monkeypatch):
+    """A failure inside the step (here: attention of layer 3) leaves lengths, tables, counts
+    and every published slot unchanged, and the step can be retried
+    (tests/unit/test_decoder.py:298-360)."""
+    weights = _synthetic(device)
+    pool = torch.full((22, 2, 6, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    requests = (RequestId("first"), RequestId("second"))
+    for request, length in zip(requests, (15, 16)):
+        allocator.create(KVReservation(request, 2))
+        dec.prefill_paged((torch.arange(length)[None] % 31).to(device), weights, allocator, request)
+    counts = allocator.capacity()
+    tables = [allocator.block_table(request) for request in requests]
+    published = pool.clone()
+    calls = 0
+    original = dec.paged_attention_batch
+
+    def failing(*args, **kwargs):
+        nonlocal calls
+        calls += 1
+        if calls == 4:
+            raise RuntimeError("injected decode failure")
+        return original(*args, **kwargs)
+
+    tokens = torch.tensor([[3], [4]], device=device)
+    monkeypatch.setattr(dec, "paged_attention_batch", failing)
+    with pytest.raises(RuntimeError, match="injected"):
+        dec.decode_paged(tokens, weights, allocator, requests)
+    monkeypatch.setattr(dec, "paged_attention_batch", original)
+    assert allocator.capacity() == counts
+    assert [allocator.block_table(request) for request in requests] == tables
+    for request, length in zip(requests, (15, 16)):
+        assert allocator.cached_length(request) == length
+        for logical, physical in enumerate(allocator.block_table(request)):
+            valid = min(16, length - logical * 16)
+            assert torch.equal(pool[:, :, physical, :valid].cpu(), published[:, :, physical, :valid].cpu())
+    logits = dec.decode_paged(tokens, weights, allocator, requests)
+    assert torch.isfinite(logits).all()
+    assert [allocator.cached_length(request) for request in requests] == [16, 17]
