@@ -147,6 +147,170 @@ def run_decode(steps: int, warmup: int, use_graph: bool = True) -> dict:
     }
 
 
+def _timed(replay, steps: int, device: torch.device) -> float:
+    """Milliseconds of `steps` calls of replay() between two HIP events on the current stream."""
+    torch.cuda.synchronize(device)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        replay()
+    stop.record()
+    torch.cuda.synchronize(device)
+    return start.elapsed_time(stop)
+
+
+def _captured(fn, device: torch.device) -> torch.cuda.CUDAGraph:
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side), torch.cuda.graph(graph, stream=side):
+        fn()
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize(device)
+    return graph
+
+
+def run_long_context(steps: int, warmup: int) -> dict:
+    """Long-context, high-occupancy decode: batch 256, every sequence at 2047 cached tokens
+    (128 blocks), a fully shuffled 40000-block pool, 22 layers. Per layer the step appends
+    each sequence's new token (pc_kv_append, slot 2047) and then runs attention over 2048
+    tokens (split-K items + merge); both are timed together, replayed as one graph."""
+    device = torch.device("cuda:0")
+    w = workloads.batched_decode(batch=256, num_blocks=40000, fixed_length=2048, seed=20261204)
+    gen = torch.Generator(device=device).manual_seed(4321)
+    pool = torch.randn((LAYERS, 2, w.num_blocks, 16, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    queries = torch.randn((LAYERS, w.batch, 32, 64), dtype=torch.float16, device=device, generator=gen)
+    new_kv = torch.randn((2, LAYERS, w.batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    out = torch.empty_like(queries)
+    lib = _hip.load()
+    max_blocks = int(w.tables.shape[1])
+    lens = torch.from_numpy(w.lengths).to(device)
+    plan = torch.from_numpy(_hip.decode_plan(w.lengths, w.tables)).to(device)
+    workspace = torch.empty(int(lib.pc_attn_workspace_bytes(w.batch, max_blocks)), dtype=torch.uint8, device=device)
+    slots = torch.from_numpy(w.tables[:, max_blocks - 1].astype(np.int64) * 16 + 15).to(device)
+    assert int(slots.max()) < w.num_blocks * 16
+
+    def step() -> None:
+        stream = torch.cuda.current_stream(device).cuda_stream
+        for layer in range(LAYERS):
+            status = lib.pc_kv_append(
+                pool.data_ptr(), w.num_blocks, layer, 1, new_kv[0, layer].data_ptr(), 0, 256,
+                new_kv[1, layer].data_ptr(), 0, 256, slots.data_ptr(), w.batch, stream,
+            )
+            status = status or lib.pc_paged_decode_attn(
+                out[layer].data_ptr(), queries[layer].data_ptr(), pool.data_ptr(), w.num_blocks, layer,
+                lens.data_ptr(), w.batch, max_blocks, plan.data_ptr(), plan.shape[0], workspace.data_ptr(), stream,
+            )
+            if status:
+                raise RuntimeError(lib.pc_last_error().decode())
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize(device)
+    eager_out = out.clone()
+    graph = _captured(step, device)
+    graph.replay()
+    torch.cuda.synchronize(device)
+    if not torch.equal(out, eager_out):
+        raise RuntimeError("graph replay differs from eager launches")
+    total_ms = _timed(graph.replay, steps, device)
+    attn = attention_bytes(w.lengths)
+    append = w.batch * 1024 * 2  # read the new K/V rows, write them to their slots
+    per_step = (attn + append) * LAYERS
+    return {
+        "workload": "batch 256, every sequence 2047 cached + 1 appended (128 blocks), 40000-block shuffled pool, "
+        "22 layers; per layer pc_kv_append of the 256 new tokens + pc_paged_decode_attn, replayed as one graph",
+        "ms_per_step": round(total_ms / steps, 4),
+        "gbps": round(per_step * steps / (total_ms / 1e3) / 1e9, 2),
+        "hbm_fraction": round(per_step * steps / (total_ms / 1e3) / 1e9 / PEAK_HBM_GBPS, 4),
+        "decode_tokens_per_s": round(w.batch * steps / (total_ms / 1e3), 1),
+        "bytes_per_layer": attn + append,
+        "us_per_layer": round(total_ms / steps / LAYERS * 1e3, 3),
+    }
+
+
+def run_decode_step(steps: int, warmup: int) -> dict:
+    """Full TinyLlama-architecture greedy decode step, batch 128, random N(0, 0.02) fp16
+    weights, contexts uniform in 256..(2048 - steps - warmup - 1) pre-filled with N(0, 1)
+    K/V in a fragmented pool; one step = embedding, 22 x (RMSNorm, QKV GEMM, RoPE + KV
+    append, paged attention, o_proj, RMSNorm, gate/up GEMM, SwiGLU, down GEMM), final norm,
+    LM head, argmax, through DecodeGraph (host bookkeeping + one graph replay per step).
+    The attention + append share replays the same 22 x (pc_rope_kv_append +
+    pc_paged_decode_attn) launches over the same inputs as a graph of their own (the
+    appended rows go to a scratch pool so the cache is not disturbed)."""
+    from pagedcore_amd import decoder as dec
+    from pagedcore_amd.engine_types import KVReservation, RequestId
+    from pagedcore_amd.kv_cache import KVAllocator
+
+    device = torch.device("cuda:0")
+    batch = 128
+    rng = workloads.rng(20261205)
+    top = 2048 - steps - warmup - 1
+    lengths = rng.integers(256, top + 1, size=batch)
+    need = int(((lengths + steps + warmup + 1 + 15) // 16).sum())
+    num_blocks = need + 256
+    weights = dec.random_weights(device=device, seed=20261205)
+    pool = torch.empty((LAYERS, 2, num_blocks, 16, 4, 64), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    requests = tuple(RequestId(f"seq{i}") for i in range(batch))
+    for request, length in zip(requests, lengths):
+        allocator.create(KVReservation(request, min(128, int((length + steps + warmup + 1 + 15) // 16))))
+    gen = torch.Generator(device=device).manual_seed(5)
+    filled = np.zeros(batch, dtype=np.int64)
+    # Appends of up to 256 tokens, requests in a fresh random order each round: every
+    # request's blocks end up interleaved with the others' (a fragmented pool).
+    while (filled < lengths).any():
+        for row in rng.permutation(batch):
+            count = int(min(256, lengths[row] - filled[row]))
+            if count > 0:
+                key = torch.randn((LAYERS, count, 4, 64), dtype=torch.float16, device=device, generator=gen)
+                value = torch.randn((LAYERS, count, 4, 64), dtype=torch.float16, device=device, generator=gen)
+                allocator.append(requests[row], key, value)
+                filled[row] += count
+    graph = dec.DecodeGraph(weights, allocator, batch)
+    ids = torch.randint(0, 32000, (batch, 1), device=device, generator=gen)
+    state = {"ids": ids}
+
+    def step() -> None:
+        state["ids"] = graph.step(state["ids"], requests).argmax(-1)
+
+    for _ in range(warmup):
+        step()
+    total_ms = _timed(step, steps, device)
+    context = int(np.sum([allocator.cached_length(r) for r in requests]))
+
+    # attention + append alone, same launches and inputs
+    scratch = torch.empty((LAYERS, 2, (batch + 15) // 16, 16, 4, 64), dtype=torch.float16, device=device)
+    scratch_slots = torch.arange(batch, dtype=torch.int64, device=device)
+    qkv = torch.randn((batch, 2560), dtype=torch.float16, device=device, generator=gen)
+    query = torch.empty((batch, 32, 64), dtype=torch.float16, device=device)
+    attention = torch.empty_like(query)
+
+    def attention_and_append() -> None:
+        for layer in range(LAYERS):
+            _hip.rope_kv_append(query, qkv, graph._inputs64[2], graph._table, pool=scratch, layer=layer, slot_mapping=scratch_slots)
+            _hip.planned_decode_attention(attention, query, pool, layer, graph._lens, graph._plan, dec.MAX_BLOCKS, graph._workspace)
+
+    attention_and_append()
+    part = _captured(attention_and_append, device)
+    part_ms = _timed(part.replay, steps, device)
+    kv_bytes = context * 1024 * LAYERS
+    weight_bytes = sum(t.numel() * 2 for layer in weights.layers for t in (dec._fused(layer).qkv, layer.o_proj, dec._fused(layer).gate_up, layer.down_proj))
+    weight_bytes += weights.lm_head.numel() * 2
+    return {
+        "workload": f"TinyLlama-architecture decode step, batch {batch}, random N(0,0.02) fp16 weights, contexts "
+        f"U{{256..{top}}} in a fragmented {num_blocks}-block pool, 22 layers, greedy argmax; DecodeGraph replay",
+        "ms_per_step": round(total_ms / steps, 4),
+        "decode_tokens_per_s": round(batch * steps / (total_ms / 1e3), 1),
+        "attention_append_ms_per_step": round(part_ms / steps, 4),
+        "attention_append_share": round(part_ms / total_ms, 4),
+        "weights_bytes": weight_bytes,
+        "kv_bytes_per_step": kv_bytes,
+        "gbps_weights_plus_kv": round((weight_bytes + kv_bytes) / (total_ms / steps / 1e3) / 1e9, 2),
+    }
+
+
 def cpu_baseline(layers: DecodeLayers, seconds: float) -> dict:
     """The oracle's op-for-op restatement of the reference torch CPU path
     (attention.py:14-53, one call per sequence as in decoder.py:182-190), run over whole
@@ -228,6 +392,9 @@ def main() -> int:
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-graph", action="store_true", help="launch from Python instead of replaying a HIP graph")
+    parser.add_argument("--workloads", default="attention,long_context,decode_step",
+                        help="comma list: attention (the headline, always run), long_context (batch 256 x 2048, append + "
+                        "attention), decode_step (full TinyLlama-architecture step, batch 128)")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="run one plain copy of this many MiB first (counter calibration under rocprofv3 --pmc)")
     args = parser.parse_args()
@@ -255,6 +422,18 @@ def main() -> int:
     baseline = None
     if not args.no_cpu_baseline:
         baseline = cpu_baseline(layers, args.cpu_seconds)
+    selected = {name.strip() for name in args.workloads.split(",")}
+    del layers, r["layers"]
+    torch.cuda.empty_cache()
+    extra = {}
+    if "long_context" in selected:
+        extra["long_context_b256"] = run_long_context(max(5, args.steps // 5), 2)
+        torch.cuda.empty_cache()
+        print(f"long context: {extra['long_context_b256']}", file=sys.stderr, flush=True)
+    if "decode_step" in selected:
+        extra["decode_step_b128"] = run_decode_step(max(10, args.steps // 2), 3)
+        torch.cuda.empty_cache()
+        print(f"decode step: {extra['decode_step_b128']}", file=sys.stderr, flush=True)
 
     record = {
         "metric": "paged-decode attn HBM GB/s (% of ~8 TB/s peak) + decode tok/s, batch 64 ctx<=2048",
@@ -295,6 +474,7 @@ def main() -> int:
             "bytes_per_launch": r["bytes_per_launch"],
         },
         "cpu_baseline": baseline,
+        **extra,
     }
     print(json.dumps(record), flush=True)
     return 0

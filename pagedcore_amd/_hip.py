@@ -152,6 +152,33 @@ def workspace_bytes(batch: int, max_blocks: int) -> int:
     return int(load().pc_attn_workspace_bytes(batch, max_blocks))
 
 
+def plan_capacity(batch: int, max_blocks: int) -> int:
+    """Records pc_attn_plan may write for this shape (its pc_attn_plan_capacity)."""
+    capacity = int(load().pc_attn_plan_capacity(batch, max_blocks))
+    if capacity < 0:
+        raise HipExtensionError(f"invalid attention shape batch={batch} max_blocks={max_blocks}")
+    return capacity
+
+
+def decode_plan_into(context_lens: np.ndarray, block_tables: np.ndarray, plan: np.ndarray) -> int:
+    """pc_attn_plan into the caller's C-contiguous int32 [capacity, record ints] array
+    (capacity >= plan_capacity of the shape); records past the returned count become
+    empty padding records, so the whole array is a valid plan of `capacity` records."""
+    lib = load()
+    lens = np.ascontiguousarray(context_lens, dtype=np.int32)
+    tables = np.ascontiguousarray(block_tables, dtype=np.int32)
+    if tables.ndim != 2 or tables.shape[0] != lens.shape[0]:
+        raise HipExtensionError("block_tables must be [batch, max_blocks] matching context_lens")
+    if plan.dtype != np.int32 or plan.ndim != 2 or plan.shape[1] != int(lib.pc_attn_plan_record_ints()) or not plan.flags.c_contiguous:
+        raise HipExtensionError("plan must be a C-contiguous int32 [capacity, record ints] array")
+    count = int(lib.pc_attn_plan(lens.ctypes.data, tables.ctypes.data, lens.shape[0], tables.shape[1], plan.ctypes.data, plan.shape[0]))
+    if count < 0:
+        _check(lib, "pc_attn_plan", -count)
+    plan[count:] = 0
+    plan[count:, 0] = -1
+    return count
+
+
 def decode_plan(context_lens: np.ndarray, block_tables: np.ndarray) -> np.ndarray:
     """Host decode plan: int32 [records, pc_attn_plan_record_ints()] from pc_attn_plan, built
     from HOST copies of the lengths [batch] and block tables [batch, max_blocks]."""
@@ -199,10 +226,25 @@ def paged_decode_attention(
         raise HipExtensionError(f"invalid attention shape batch={batch} max_blocks={max_blocks}")
     if workspace is None:
         workspace = attention_workspace(pool.device, nbytes)
-    elif workspace.numel() * workspace.element_size() < nbytes:
-        raise HipExtensionError(f"workspace needs {nbytes} bytes")
     if plan is None:
         plan = torch.from_numpy(decode_plan(context_lens.cpu().numpy(), block_tables.cpu().numpy())).to(pool.device)
+    planned_decode_attention(out, query, pool, layer, context_lens, plan, max_blocks, workspace)
+
+
+def planned_decode_attention(
+    out: Tensor, query: Tensor, pool: Tensor, layer: int, context_lens: Tensor, plan: Tensor, max_blocks: int,
+    workspace: Tensor,
+) -> None:
+    """pc_paged_decode_attn with a ready device plan (decode_plan() rows, possibly padded
+    with empty records) for a batch of context_lens.shape[0] rows whose tables are at most
+    max_blocks wide; workspace of workspace_bytes(batch, max_blocks) bytes."""
+    lib = load()
+    batch = int(context_lens.shape[0])
+    nbytes = int(lib.pc_attn_workspace_bytes(batch, max_blocks))
+    if nbytes <= 0:
+        raise HipExtensionError(f"invalid attention shape batch={batch} max_blocks={max_blocks}")
+    if workspace.numel() * workspace.element_size() < nbytes:
+        raise HipExtensionError(f"workspace needs {nbytes} bytes")
     if (
         plan.dtype != torch.int32
         or plan.dim() != 2

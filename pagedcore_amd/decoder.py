@@ -287,6 +287,141 @@ def decode_paged(
 
 
 # ---------------------------------------------------------------------------------------
+# Decode as one replayed HIP graph
+# ---------------------------------------------------------------------------------------
+
+MAX_BLOCKS = CONTEXT_LIMIT // 16  # 128: the widest block table of a request
+
+
+class DecodeGraph:
+    """decode_paged for a fixed batch size, captured once as a HIP graph and replayed.
+
+    A decode step is about 200 launches (9 per layer); issued one by one from Python they
+    cost more host time than the GPU needs to run them. Here the step's device work is
+    captured once, with every per-step input in static device buffers: token ids, the
+    staged token's slot and position of each row, the staged context lengths, and the
+    decode plan at its full capacity (pc_attn_plan_capacity records for the batch and
+    128-block tables, the tail padded with empty records). Per step the host does the
+    allocator's staged-append bookkeeping, builds the plan into a pinned buffer, uploads
+    it with two asynchronous copies and replays the graph; nothing synchronizes.
+
+    Same results, checks, errors and staged-append semantics as decode_paged for a batch
+    of `batch` requests (any requests, in any order, step to step); the kernels and their
+    shapes are the same, so the logits and cache bytes equal decode_paged's.
+    """
+
+    def __init__(self, weights: TinyLlamaWeights, allocator: KVAllocator, batch: int) -> None:
+        _check_weights(weights, "decode")
+        if type(batch) is not int or batch < 1:
+            raise ValueError("batch must be a positive integer")
+        _check_gpu(allocator, weights, "decode")
+        device = allocator.pool.device
+        self.batch = batch
+        self._weights = weights
+        self._allocator = allocator
+        self._table = rope_table(device)
+        fields = int(_hip.load().pc_attn_plan_record_ints())
+        self._capacity = _hip.plan_capacity(batch, MAX_BLOCKS)
+        # Static graph inputs: int64 [3, B] = token ids, slots, positions; int32
+        # [lens_span + capacity * fields] = context lengths (padded to 256 B, which keeps
+        # the plan records aligned), then the plan records.
+        self._lens_span = (batch + 63) // 64 * 64
+        self._inputs64 = torch.zeros((3, batch), dtype=torch.int64, device=device)
+        self._inputs64[1].fill_(-1)  # no slot: warm-up and capture write nothing to the pool
+        self._inputs32 = torch.zeros(self._lens_span + self._capacity * fields, dtype=torch.int32, device=device)
+        self._lens = self._inputs32[:batch]
+        self._plan = self._inputs32[self._lens_span :].view(self._capacity, fields)
+        self._plan[:, 0] = -1
+        self._workspace = torch.empty(max(256, _hip.workspace_bytes(batch, MAX_BLOCKS)), dtype=torch.uint8, device=device)
+        # Two pinned staging buffers used in turn; an event marks when a buffer's upload
+        # has run, so it is not refilled while its copy may still be pending.
+        self._host = [
+            (
+                torch.empty((3, batch), dtype=torch.int64, pin_memory=True),
+                torch.zeros(self._lens_span + self._capacity * fields, dtype=torch.int32, pin_memory=True),
+            )
+            for _ in range(2)
+        ]
+        self._uploaded: list = [None, None]
+        self._turn = 0
+
+        stream = torch.cuda.current_stream(device)
+        self._forward()  # eager warm-up: library initialisation and GEMM selection happen outside the capture
+        torch.cuda.synchronize(device)
+        self._graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(device=device)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side), torch.cuda.graph(self._graph, stream=side):
+            self._logits = self._forward()
+        stream.wait_stream(side)
+        torch.cuda.synchronize(device)
+
+    def _forward(self) -> Tensor:
+        """The step's device work over the static inputs (eager, or under capture)."""
+        weights = self._weights
+        pool = self._allocator.pool
+        batch = self.batch
+        ids, slots, positions = self._inputs64
+        hidden = F.embedding(ids, weights.embedding)
+        x = torch.empty_like(hidden)
+        _hip.add_rms_norm(x, hidden, None, weights.layers[0].input_norm, RMS_EPS)
+        query = torch.empty((batch, Q_HEADS, HEAD_DIM), dtype=torch.float16, device=pool.device)
+        attention = torch.empty_like(query)
+        for index, layer in enumerate(weights.layers):
+            fused = _fused(layer)
+            qkv = F.linear(x, fused.qkv)
+            _hip.rope_kv_append(query, qkv, positions, self._table, pool=pool, layer=index, slot_mapping=slots)
+            _hip.planned_decode_attention(attention, query, pool, index, self._lens, self._plan, MAX_BLOCKS, self._workspace)
+            projected = F.linear(attention.view(batch, HIDDEN), layer.o_proj)
+            _hip.add_rms_norm(x, hidden, projected, layer.post_attention_norm, RMS_EPS)
+            gate_up = F.linear(x, fused.gate_up)
+            activated = torch.empty((batch, gate_up.shape[1] // 2), dtype=torch.float16, device=pool.device)
+            _hip.silu_mul(activated, gate_up)
+            down = F.linear(activated, layer.down_proj)
+            following = weights.layers[index + 1].input_norm if index + 1 < LAYERS else weights.final_norm
+            _hip.add_rms_norm(x, hidden, down, following, RMS_EPS)
+        return F.linear(x, weights.lm_head)
+
+    @torch.inference_mode()
+    def step(self, input_ids: Tensor, request_ids: Tuple[RequestId, ...]) -> Tensor:
+        """decode_paged(input_ids, weights, allocator, request_ids) by graph replay; the
+        batch must have the captured size. Returns fresh fp16 logits [B, 1, vocab]."""
+        request_ids = tuple(request_ids)
+        if input_ids.dtype != torch.int64 or input_ids.ndim != 2 or input_ids.shape != (len(request_ids), 1):
+            raise ValueError("input_ids must be int64 [batch, 1] matching request IDs")
+        if input_ids.device != self._weights.embedding.device:
+            raise ValueError("input_ids and weights must be on the same device")
+        if len(request_ids) != self.batch:
+            raise ValueError(f"this decode graph runs batches of {self.batch} requests")
+        allocator = self._allocator
+        for request_id in request_ids:
+            allocator.cached_length(request_id)  # KeyError for an unknown request
+        with allocator.append_decode(request_ids):
+            staged = allocator.staged_decode(request_ids, width=MAX_BLOCKS)
+            turn = self._turn
+            self._turn ^= 1
+            if self._uploaded[turn] is not None:
+                self._uploaded[turn].synchronize()
+            host64, host32 = self._host[turn]
+            h64 = host64.numpy()
+            h32 = host32.numpy()
+            h64[1] = staged.slots
+            h64[2] = staged.positions
+            h32[: self.batch] = staged.lengths
+            _hip.decode_plan_into(staged.lengths, staged.tables, h32[self._lens_span :].reshape(self._capacity, -1))
+            self._inputs64[1:].copy_(host64[1:], non_blocking=True)
+            self._inputs32.copy_(host32, non_blocking=True)
+            uploaded = torch.cuda.Event()
+            uploaded.record()
+            self._uploaded[turn] = uploaded
+            self._inputs64[0].copy_(input_ids[:, 0])
+            self._graph.replay()
+            allocator.record_decode_writes(request_ids, LAYERS)
+            logits = self._logits.clone()
+        return logits.unsqueeze(1)
+
+
+# ---------------------------------------------------------------------------------------
 # Prefill
 # ---------------------------------------------------------------------------------------
 

@@ -126,6 +126,16 @@ class _HostOnlyWriter:
         )
 
 
+@dataclass(frozen=True)
+class StagedDecode:
+    """Host arrays of a staged decode step (KVAllocator.staged_decode)."""
+
+    slots: np.ndarray  # int64 [B]: block * 16 + offset of each request's new position
+    positions: np.ndarray  # int64 [B]: that position (the cached length before the step)
+    lengths: np.ndarray  # int32 [B]: staged lengths (cached length + 1)
+    tables: np.ndarray  # int32 [B, width]: staged block tables in logical order, zero padded
+
+
 @dataclass(slots=True)
 class _DecodeBatch:
     """Device block tables and lengths of one batch of requests, plus their host copies
@@ -513,6 +523,58 @@ class KVAllocator:
         result = (both[0], both[1])
         self._decode_slot_cache[request_ids] = result
         return result
+
+    def staged_decode(self, request_ids: Sequence[RequestId], *, width: Optional[int] = None) -> "StagedDecode":
+        """Host view of the staged decode step, for callers that enqueue the step's KV
+        writes and reads themselves (a captured HIP graph replayed on this allocator's
+        stream): per row, the slot and position of the request's new token, its staged
+        length and its staged block table (zero padded to `width`, default the widest).
+
+        Pair with record_decode_writes once the writes are enqueued.
+        """
+        self._check_worker()
+        self._check_staged_state()
+        if self._decode_appends is None:
+            raise RuntimeError("decode writes require a staged append")
+        if not request_ids or len(set(request_ids)) != len(request_ids):
+            raise ValueError("decode requires nonempty, distinct request IDs")
+        appends = [self._decode_appends[request_id] for request_id in request_ids]
+        sequences = [append.sequence for append in appends]
+        widest = max(len(sequence.blocks) for sequence in sequences)
+        if width is None:
+            width = widest
+        elif widest > width:
+            raise ValueError("staged block tables are wider than the requested width")
+        tables = np.zeros((len(sequences), width), dtype=np.int32)
+        lengths = np.empty(len(sequences), dtype=np.int32)
+        slots = np.empty(len(sequences), dtype=np.int64)
+        positions = np.empty(len(sequences), dtype=np.int64)
+        for row, sequence in enumerate(sequences):
+            tables[row, : len(sequence.blocks)] = sequence.blocks
+            lengths[row] = sequence.length
+            positions[row] = sequence.length - 1
+            logical_block, offset = divmod(sequence.length - 1, BLOCK_TOKENS)
+            slots[row] = sequence.blocks[logical_block] * BLOCK_TOKENS + offset
+        return StagedDecode(slots, positions, lengths, tables)
+
+    def record_decode_writes(self, request_ids: Sequence[RequestId], layers: int = LAYERS) -> None:
+        """Record that the caller has enqueued, on this allocator's stream, the staged
+        token's K/V writes of layers [0, layers) for every request (each layer's write
+        ahead of any read of that layer), as write_decode_layers would have. Layers are
+        still written once and in order: every request must be at layer 0."""
+        self._check_worker()
+        self._check_staged_state()
+        if self._decode_appends is None:
+            raise RuntimeError("decode writes require a staged append")
+        if not request_ids or len(set(request_ids)) != len(request_ids):
+            raise ValueError("decode requires nonempty, distinct request IDs")
+        appends = [self._decode_appends[request_id] for request_id in request_ids]
+        if type(layers) is not int or not 0 < layers <= LAYERS:
+            raise ValueError("layers must count 1 to 22 decoder layers")
+        if any(append.written_layers != 0 for append in appends):
+            raise ValueError("decode cache layers must be written once in order")
+        for append in appends:
+            append.written_layers = layers
 
     def iter_layer_blocks(
         self, request_id: RequestId, *, layer_index: int

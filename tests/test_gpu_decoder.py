@@ -380,3 +380,43 @@ def test_decode_paged_failure_discards_the_step(device, monkeypatch):
     logits = dec.decode_paged(tokens, weights, allocator, requests)
     assert torch.isfinite(logits).all()
     assert [allocator.cached_length(request) for request in requests] == [16, 17]
+
+
+def test_decode_graph_replays_equal_decode_paged(device):
+    """DecodeGraph (one captured HIP graph per step) against eager decode_paged on a twin
+    pool: bit-identical logits and pool bytes over several steps, with the request order
+    changing and a request replaced between steps, eager GPU work and synchronizations in
+    between replays."""
+    weights = _synthetic(device)
+    lengths = (1, 15, 16, 17, 49, 200, 2040)
+    pools = [torch.full((22, 2, 176, 16, 4, 64), float("nan"), dtype=torch.float16, device=device) for _ in range(2)]
+    eager, graphed = (KVAllocator(pool) for pool in pools)
+    requests = [RequestId(f"g{row}") for row in range(len(lengths))]
+
+    def admit(request, length):
+        ids = ((torch.arange(length)[None] * 3 + length) % 31).to(device)
+        for allocator in (eager, graphed):
+            allocator.create(KVReservation(request, (length + 6 + 15) // 16))
+            dec.prefill_paged(ids, weights, allocator, request)
+
+    for request, length in zip(requests, lengths):
+        admit(request, length)
+    graph = dec.DecodeGraph(weights, graphed, batch=len(lengths))
+    with pytest.raises(ValueError, match="batches of 7"):
+        graph.step(torch.zeros((2, 1), dtype=torch.int64, device=device), tuple(requests[:2]))
+    for step in range(5):
+        if step == 3:  # replace a request between steps
+            for allocator in (eager, graphed):
+                allocator.release_all(requests[2])
+            requests[2] = RequestId("late")
+            admit(requests[2], 33)
+        order = tuple(requests) if step % 2 == 0 else tuple(reversed(requests))
+        tokens = torch.tensor([[(5 * step + row) % 31] for row in range(len(order))], device=device)
+        expected = dec.decode_paged(tokens, weights, eager, order)
+        got = graph.step(tokens, order)
+        torch.cuda.synchronize()
+        assert torch.equal(got, expected)
+        assert torch.equal(pools[0].view(torch.int16), pools[1].view(torch.int16))
+        assert graphed.capacity() == eager.capacity()
+        assert [graphed.cached_length(r) for r in order] == [eager.cached_length(r) for r in order]
+        torch.randn(1000, device=device).sum().item()  # unrelated eager work between replays
