@@ -230,6 +230,56 @@ def run_long_context(steps: int, warmup: int) -> dict:
     }
 
 
+def run_prompt_append(steps: int) -> dict:
+    """Prompt KV append: one 2048-token prompt's K and V (22 layers, N(0, 1) fp16) into a
+    4096-block pool whose free list is in seeded random order with 30% of it held by 10
+    filler requests, so the prompt's 128 blocks are scattered. The allocator's append is
+    called once (its slot mapping); the timed region replays that one pc_kv_append launch
+    (all 22 layers x 2048 tokens) as a graph of `steps` launches."""
+    from pagedcore_amd.engine_types import KVReservation, RequestId
+    from pagedcore_amd.kv_cache import KVAllocator
+
+    device = torch.device("cuda:0")
+    w = workloads.prompt_append()
+    pool = torch.zeros((LAYERS, 2, w.num_blocks, 16, 4, 64), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    allocator._free_blocks[:] = w.free_order  # the seeded allocator's free-list order
+    for index in range(len(w.filler_blocks)):
+        request = RequestId(f"filler{index}")
+        allocator.create(KVReservation(request, w.filler_blocks[index]))
+        allocator.append(request, *(torch.from_numpy(a).to(device) for a in w.filler_kv(index)))
+    key, value = (torch.from_numpy(a).to(device) for a in w.prompt_kv())
+    prompt = RequestId("prompt")
+    allocator.create(KVReservation(prompt, 128))
+    torch.cuda.synchronize(device)
+    start = time.perf_counter()
+    allocator.append(prompt, key, value)
+    torch.cuda.synchronize(device)
+    api_ms = (time.perf_counter() - start) * 1e3
+    table = np.asarray(allocator.block_table(prompt), dtype=np.int64)
+    positions = np.arange(w.prompt_tokens)
+    slots = torch.from_numpy(table[positions // 16] * 16 + positions % 16).to(device)
+    scattered = int(np.sum(np.diff(table) != 1))
+
+    def launches() -> None:
+        for _ in range(steps):
+            _hip.kv_append(pool, 0, key, value, slots)
+
+    graph = _captured(launches, device)
+    total_ms = _timed(graph.replay, 1, device)
+    nbytes = 2 * 2 * LAYERS * w.prompt_tokens * 256 * 2  # K and V, read once and written once
+    us = total_ms / steps * 1e3
+    return {
+        "workload": "2048-token prompt x 22 layers (K and V [22,2048,4,64] fp16) into a 4096-block pool, 30% held by "
+        f"10 filler requests, free list in seeded random order ({scattered} discontinuities in the 128-block table)",
+        "us_per_append": round(us, 3),
+        "gbps": round(nbytes / (us / 1e6) / 1e9, 2),
+        "hbm_fraction": round(nbytes / (us / 1e6) / 1e9 / PEAK_HBM_GBPS, 4),
+        "bytes_per_append": nbytes,
+        "allocator_append_ms": round(api_ms, 3),
+    }
+
+
 def run_decode_step(steps: int, warmup: int) -> dict:
     """Full TinyLlama-architecture greedy decode step, batch 128, random N(0, 0.02) fp16
     weights, contexts uniform in 256..(2048 - steps - warmup - 1) pre-filled with N(0, 1)
@@ -384,6 +434,24 @@ def calibration_copy(mib: int, device: torch.device) -> None:
     del src, dst
 
 
+def run_extra(selected: set, steps: int) -> dict:
+    """The workloads beside the headline, each reported as its own object."""
+    extra = {}
+    if "prompt_append" in selected:
+        extra["prompt_append"] = run_prompt_append(max(10, steps))
+        torch.cuda.empty_cache()
+        print(f"prompt append: {extra['prompt_append']}", file=sys.stderr, flush=True)
+    if "long_context" in selected:
+        extra["long_context_b256"] = run_long_context(max(5, steps // 5), 2)
+        torch.cuda.empty_cache()
+        print(f"long context: {extra['long_context_b256']}", file=sys.stderr, flush=True)
+    if "decode_step" in selected:
+        extra["decode_step_b128"] = run_decode_step(max(10, steps // 2), 3)
+        torch.cuda.empty_cache()
+        print(f"decode step: {extra['decode_step_b128']}", file=sys.stderr, flush=True)
+    return extra
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -392,9 +460,10 @@ def main() -> int:
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-graph", action="store_true", help="launch from Python instead of replaying a HIP graph")
-    parser.add_argument("--workloads", default="attention,long_context,decode_step",
-                        help="comma list: attention (the headline, always run), long_context (batch 256 x 2048, append + "
-                        "attention), decode_step (full TinyLlama-architecture step, batch 128)")
+    parser.add_argument("--workloads", default="attention,prompt_append,long_context,decode_step",
+                        help="comma list: attention (the headline; without it only the others run, as a diagnostic line), prompt_append (2048-token prompt into a "
+                        "fragmented pool), long_context (batch 256 x 2048, append + attention), decode_step (full "
+                        "TinyLlama-architecture step, batch 128)")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="run one plain copy of this many MiB first (counter calibration under rocprofv3 --pmc)")
     args = parser.parse_args()
@@ -409,6 +478,17 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.calibrate_copy_mib > 0:
         calibration_copy(args.calibrate_copy_mib, torch.device("cuda:0"))
+    selected = {name.strip() for name in args.workloads.split(",")}
+    unknown = selected - {"attention", "prompt_append", "long_context", "decode_step"}
+    if unknown:
+        print(f"unknown workloads {sorted(unknown)}", file=sys.stderr)
+        return 2
+    if "attention" not in selected:
+        # Diagnostic run of the other workloads alone (e.g. to profile one of them); the
+        # headline line needs the attention workload.
+        extra = run_extra(selected, args.steps)
+        print(json.dumps({"diagnostic": True, **extra}), flush=True)
+        return 0
     r = run_decode(args.steps, args.warmup, use_graph=not args.no_graph)
     w, layers = r["w"], r["layers"]
     print(
@@ -422,18 +502,9 @@ def main() -> int:
     baseline = None
     if not args.no_cpu_baseline:
         baseline = cpu_baseline(layers, args.cpu_seconds)
-    selected = {name.strip() for name in args.workloads.split(",")}
     del layers, r["layers"]
     torch.cuda.empty_cache()
-    extra = {}
-    if "long_context" in selected:
-        extra["long_context_b256"] = run_long_context(max(5, args.steps // 5), 2)
-        torch.cuda.empty_cache()
-        print(f"long context: {extra['long_context_b256']}", file=sys.stderr, flush=True)
-    if "decode_step" in selected:
-        extra["decode_step_b128"] = run_decode_step(max(10, args.steps // 2), 3)
-        torch.cuda.empty_cache()
-        print(f"decode step: {extra['decode_step_b128']}", file=sys.stderr, flush=True)
+    extra = run_extra(selected, args.steps)
 
     record = {
         "metric": "paged-decode attn HBM GB/s (% of ~8 TB/s peak) + decode tok/s, batch 64 ctx<=2048",
