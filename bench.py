@@ -280,6 +280,54 @@ def run_prompt_append(steps: int) -> dict:
     }
 
 
+def run_prefill(steps: int) -> dict:
+    """Paged prefill of one 2048-token prompt through the full TinyLlama-architecture model
+    (random N(0, 0.02) fp16 weights): prefill_paged = 22 x (RMSNorm, QKV GEMM, RoPE + KV write
+    into the staged slots, causal prompt attention, o_proj, add + RMSNorm, gate/up GEMM,
+    SwiGLU, down GEMM, add + RMSNorm), LM head over all positions, one publish. Timed end to
+    end per prompt (the request is released and re-admitted between prompts, untimed),
+    plus the prompt attention kernel alone on the same shapes."""
+    from pagedcore_amd import decoder as dec
+    from pagedcore_amd.engine_types import KVReservation, RequestId
+    from pagedcore_amd.kv_cache import KVAllocator
+
+    device = torch.device("cuda:0")
+    tokens = 2048
+    weights = dec.random_weights(device=device, seed=20261206)
+    pool = torch.empty((LAYERS, 2, 160, 16, 4, 64), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    gen = torch.Generator(device=device).manual_seed(6)
+    ids = torch.randint(0, 32000, (1, tokens), device=device, generator=gen)
+    request = RequestId("prompt")
+    total = 0.0
+    for index in range(steps + 1):
+        allocator.create(KVReservation(request, tokens // 16))
+        torch.cuda.synchronize(device)
+        start = time.perf_counter()
+        dec.prefill_paged(ids, weights, allocator, request)
+        torch.cuda.synchronize(device)
+        if index > 0:  # the first prompt warms up the GEMM libraries
+            total += time.perf_counter() - start
+        allocator.release_all(request)
+    ms = total / steps * 1e3
+
+    query = torch.randn((tokens, 32, 64), dtype=torch.float16, device=device, generator=gen)
+    key = torch.randn((tokens, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    value = torch.randn((tokens, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    out = torch.empty_like(query)
+    graph = _captured(lambda: [_hip.prefill_attention(out, query, key, value) for _ in range(10)], device)
+    attn_us = _timed(graph.replay, 3, device) / 30 * 1e3
+    flops = tokens * (tokens + 1) // 2 * 32 * 64 * 2 * 2
+    return {
+        "workload": "paged prefill of one 2048-token prompt, TinyLlama-architecture random N(0,0.02) fp16 weights, "
+        "22 layers, RoPE + KV write fused into the staged append, causal prompt attention kernel",
+        "ms_per_prompt": round(ms, 3),
+        "prompt_tokens_per_s": round(tokens / (ms / 1e3), 1),
+        "prompt_attention_us_per_layer": round(attn_us, 2),
+        "prompt_attention_tflops": round(flops / (attn_us / 1e6) / 1e12, 2),
+    }
+
+
 def run_decode_step(steps: int, warmup: int) -> dict:
     """Full TinyLlama-architecture greedy decode step, batch 128, random N(0, 0.02) fp16
     weights, contexts uniform in 256..(2048 - steps - warmup - 1) pre-filled with N(0, 1)
@@ -445,6 +493,10 @@ def run_extra(selected: set, steps: int) -> dict:
         extra["long_context_b256"] = run_long_context(max(5, steps // 5), 2)
         torch.cuda.empty_cache()
         print(f"long context: {extra['long_context_b256']}", file=sys.stderr, flush=True)
+    if "prefill" in selected:
+        extra["prefill_2048"] = run_prefill(5)
+        torch.cuda.empty_cache()
+        print(f"prefill: {extra['prefill_2048']}", file=sys.stderr, flush=True)
     if "decode_step" in selected:
         extra["decode_step_b128"] = run_decode_step(max(10, steps // 2), 3)
         torch.cuda.empty_cache()
@@ -460,10 +512,10 @@ def main() -> int:
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-graph", action="store_true", help="launch from Python instead of replaying a HIP graph")
-    parser.add_argument("--workloads", default="attention,prompt_append,long_context,decode_step",
+    parser.add_argument("--workloads", default="attention,prompt_append,long_context,prefill,decode_step",
                         help="comma list: attention (the headline; without it only the others run, as a diagnostic line), prompt_append (2048-token prompt into a "
-                        "fragmented pool), long_context (batch 256 x 2048, append + attention), decode_step (full "
-                        "TinyLlama-architecture step, batch 128)")
+                        "fragmented pool), long_context (batch 256 x 2048, append + attention), prefill (one 2048-token "
+                        "prompt through the model), decode_step (full TinyLlama-architecture step, batch 128)")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="run one plain copy of this many MiB first (counter calibration under rocprofv3 --pmc)")
     args = parser.parse_args()
@@ -479,7 +531,7 @@ def main() -> int:
     if args.calibrate_copy_mib > 0:
         calibration_copy(args.calibrate_copy_mib, torch.device("cuda:0"))
     selected = {name.strip() for name in args.workloads.split(",")}
-    unknown = selected - {"attention", "prompt_append", "long_context", "decode_step"}
+    unknown = selected - {"attention", "prompt_append", "long_context", "prefill", "decode_step"}
     if unknown:
         print(f"unknown workloads {sorted(unknown)}", file=sys.stderr)
         return 2

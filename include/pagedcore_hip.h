@@ -175,6 +175,22 @@ int pc_add_rms_norm(void* out, void* hidden, const void* delta, const void* weig
  */
 int pc_silu_mul(void* out, const void* gate_up, int64_t rows, int32_t width, void* stream);
 
+/*
+ * Causal attention of one prompt over its contiguous K/V (the prefill of one sequence).
+ *
+ * Replaces the prompt's dense_attention (reference src/pagedcore/dense.py:69-81, called by
+ * the prefill forward at src/pagedcore/decoder.py:236-237):
+ *   out[t][h] = softmax_{j <= t}(query[t][h] . key[j][h / 8] / 8) . value[j][h / 8]
+ * query, out: [tokens][32][64] fp16; key, value: [tokens][4][64] fp16 (the rotated keys and
+ * the values of pc_rope_kv_append's key_out / value_out); all contiguous, 16-byte aligned;
+ * tokens in [0, 65536]. Scores, softmax and the weighted sum are fp32 (online softmax,
+ * probabilities enter the PV product as fp16) with one final fp16 rounding, where the
+ * reference rounds the scores and the normalised probabilities to fp16 (the accepted
+ * difference is within the decoder tolerances).
+ */
+int pc_prefill_attention(void* out, const void* query, const void* key, const void* value, int32_t tokens,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

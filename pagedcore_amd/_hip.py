@@ -17,7 +17,7 @@ import numpy as np
 import torch
 from torch import Tensor
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 LIBRARY_NAME = "libpagedcore_hip.so"
 
 _lock = threading.Lock()
@@ -59,6 +59,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pc_add_rms_norm.argtypes = [_p, _p, _p, _p, _i64, _i32, ctypes.c_float, _p]
     lib.pc_silu_mul.restype = ctypes.c_int
     lib.pc_silu_mul.argtypes = [_p, _p, _i64, _i32, _p]
+    lib.pc_prefill_attention.restype = ctypes.c_int
+    lib.pc_prefill_attention.argtypes = [_p, _p, _p, _p, _i32, _p]
 
 
 def load() -> ctypes.CDLL:
@@ -332,3 +334,22 @@ def silu_mul(out: Tensor, gate_up: Tensor) -> None:
     lib = load()
     status = lib.pc_silu_mul(out.data_ptr(), gate_up.data_ptr(), out.shape[0], out.shape[1], _stream(out.device))
     _check(lib, "pc_silu_mul", status)
+
+
+def prefill_attention(out: Tensor, query: Tensor, key: Tensor, value: Tensor) -> None:
+    """Causal attention of one prompt: out/query contiguous fp16 [T, 32, 64], key/value
+    contiguous fp16 [T, 4, 64], on one device; enqueued on its current stream."""
+    lib = load()
+    tokens = int(query.shape[0])
+    if (
+        query.shape != (tokens, 32, 64)
+        or out.shape != query.shape
+        or key.shape != (tokens, 4, 64)
+        or value.shape != key.shape
+        or not all(t.is_contiguous() and t.dtype == torch.float16 for t in (out, query, key, value))
+    ):
+        raise HipExtensionError("prefill attention needs contiguous fp16 [T, 32, 64] query/out and [T, 4, 64] K/V")
+    status = lib.pc_prefill_attention(
+        out.data_ptr(), query.data_ptr(), key.data_ptr(), value.data_ptr(), tokens, _stream(query.device)
+    )
+    _check(lib, "pc_prefill_attention", status)

@@ -426,26 +426,6 @@ class DecodeGraph:
 # ---------------------------------------------------------------------------------------
 
 
-def _dense_causal_attention(query: Tensor, key: Tensor, value: Tensor) -> Tensor:
-    """Prompt attention with the reference's fp16 rounding (src/pagedcore/dense.py:69-81):
-    fp16 scores scaled by 1/8, causal mask, fp32 softmax rounded to fp16, fp16 product.
-
-    query [T, 32, 64], key/value [T, 4, 64] (rotated K) -> [T, 2048]. The 8 query heads of
-    kv head g share it through a reshape instead of a repeat_interleave copy.
-    """
-    tokens = query.shape[0]
-    group = Q_HEADS // KV_HEADS
-    q = query.view(tokens, KV_HEADS, group, HEAD_DIM).permute(1, 2, 0, 3).reshape(KV_HEADS, group * tokens, HEAD_DIM)
-    k = key.permute(1, 2, 0).contiguous()  # [4, 64, T]
-    v = value.permute(1, 0, 2).contiguous()  # [4, T, 64]
-    scores = torch.matmul(q.contiguous(), k) * (HEAD_DIM**-0.5)  # [4, 8T, T] fp16
-    allowed = torch.ones((tokens, tokens), dtype=torch.bool, device=query.device).tril()
-    scores = scores.view(KV_HEADS, group, tokens, tokens).masked_fill(~allowed, torch.finfo(torch.float16).min)
-    probabilities = F.softmax(scores, dim=-1, dtype=torch.float32).to(torch.float16)
-    out = torch.matmul(probabilities.view(KV_HEADS, group * tokens, tokens), v)  # [4, 8T, 64]
-    return out.view(KV_HEADS, group, tokens, HEAD_DIM).permute(2, 0, 1, 3).reshape(tokens, HIDDEN)
-
-
 @torch.inference_mode()
 def prefill_paged(
     input_ids: Tensor,
@@ -454,8 +434,13 @@ def prefill_paged(
     request_id: RequestId,
 ) -> Tensor:
     """Prefill one admitted, empty request from int64 [1, T] prompt ids; returns fp16
-    logits [1, T, vocab]. Only K is rotated; the prompt's K/V are published through one
-    allocator.append after the forward succeeds (reference src/pagedcore/decoder.py:113-135).
+    logits [1, T, vocab]. Only K is rotated (reference src/pagedcore/decoder.py:113-135).
+
+    The K/V write is fused into the forward: per layer, pc_rope_kv_append rotates Q and K
+    and writes the rotated K and the V straight into the slots the append takes (staged
+    through KVAllocator.append_prompt), besides the contiguous copy the prompt's attention
+    reads. The append is published only after the whole forward succeeded, as the
+    reference publishes its one append after the forward.
     """
     if allocator.cached_length(request_id) != 0:
         raise ValueError("paged prefill requires an empty request cache")
@@ -470,26 +455,31 @@ def prefill_paged(
     _check_gpu(allocator, weights, "prefill")
     device = input_ids.device
     table = rope_table(device)
-    positions = torch.arange(tokens, dtype=torch.int64, device=device)
-    hidden = F.embedding(input_ids[0], weights.embedding)  # [T, 2048]
-    x = torch.empty_like(hidden)
-    _hip.add_rms_norm(x, hidden, None, weights.layers[0].input_norm, RMS_EPS)
-    keys = torch.empty((LAYERS, tokens, KV_HEADS, HEAD_DIM), dtype=torch.float16, device=device)
-    values = torch.empty_like(keys)
-    query = torch.empty((tokens, Q_HEADS, HEAD_DIM), dtype=torch.float16, device=device)
-    for index, layer in enumerate(weights.layers):
-        fused = _fused(layer)
-        qkv = F.linear(x, fused.qkv)
-        _hip.rope_kv_append(query, qkv, positions, table, key_out=keys[index], value_out=values[index])
-        attention = _dense_causal_attention(query, keys[index], values[index])
-        projected = F.linear(attention, layer.o_proj)
-        _hip.add_rms_norm(x, hidden, projected, layer.post_attention_norm, RMS_EPS)
-        gate_up = F.linear(x, fused.gate_up)
-        activated = torch.empty((tokens, gate_up.shape[1] // 2), dtype=torch.float16, device=device)
-        _hip.silu_mul(activated, gate_up)
-        down = F.linear(activated, layer.down_proj)
-        following = weights.layers[index + 1].input_norm if index + 1 < LAYERS else weights.final_norm
-        _hip.add_rms_norm(x, hidden, down, following, RMS_EPS)
-    logits = F.linear(x, weights.lm_head)
-    allocator.append(request_id, keys, values)
+    pool = allocator.pool
+    with allocator.append_prompt(request_id, tokens) as staged:
+        hidden = F.embedding(input_ids[0], weights.embedding)  # [T, 2048]
+        x = torch.empty_like(hidden)
+        _hip.add_rms_norm(x, hidden, None, weights.layers[0].input_norm, RMS_EPS)
+        key = torch.empty((tokens, KV_HEADS, HEAD_DIM), dtype=torch.float16, device=device)
+        value = torch.empty_like(key)
+        query = torch.empty((tokens, Q_HEADS, HEAD_DIM), dtype=torch.float16, device=device)
+        attended = torch.empty_like(query)
+        for index, layer in enumerate(weights.layers):
+            fused = _fused(layer)
+            qkv = F.linear(x, fused.qkv)
+            _hip.rope_kv_append(
+                query, qkv, staged.positions, table, key_out=key, value_out=value, pool=pool, layer=index,
+                slot_mapping=staged.slot_mapping,
+            )
+            staged.record_layer(index)
+            _hip.prefill_attention(attended, query, key, value)
+            projected = F.linear(attended.view(tokens, HIDDEN), layer.o_proj)
+            _hip.add_rms_norm(x, hidden, projected, layer.post_attention_norm, RMS_EPS)
+            gate_up = F.linear(x, fused.gate_up)
+            activated = torch.empty((tokens, gate_up.shape[1] // 2), dtype=torch.float16, device=device)
+            _hip.silu_mul(activated, gate_up)
+            down = F.linear(activated, layer.down_proj)
+            following = weights.layers[index + 1].input_norm if index + 1 < LAYERS else weights.final_norm
+            _hip.add_rms_norm(x, hidden, down, following, RMS_EPS)
+        logits = F.linear(x, weights.lm_head)
     return logits.unsqueeze(0)

@@ -126,6 +126,23 @@ class _HostOnlyWriter:
         )
 
 
+@dataclass
+class StagedPrompt:
+    """A prompt append staged by KVAllocator.append_prompt: the caller writes each layer's
+    K/V to `slot_mapping` itself and records it with record_layer, in layer order."""
+
+    request_id: RequestId
+    tokens: int
+    slot_mapping: Tensor  # int64 [tokens]: block * 16 + offset of each new position
+    positions: Tensor  # int64 [tokens]: the new positions (cached length .. + tokens - 1)
+    written_layers: int = 0
+
+    def record_layer(self, layer_index: int) -> None:
+        if type(layer_index) is not int or layer_index != self.written_layers or layer_index >= LAYERS:
+            raise ValueError("prompt cache layers must be written once in order")
+        self.written_layers += 1
+
+
 @dataclass(frozen=True)
 class StagedDecode:
     """Host arrays of a staged decode step (KVAllocator.staged_decode)."""
@@ -236,6 +253,7 @@ class KVAllocator:
         # (container identities and mutation counts, counts) of the last verified state.
         self._verified: Optional[Tuple[tuple, CapacityCounts]] = None
         self._decode_appends: Optional[Dict[RequestId, _TokenAppend]] = None
+        self._prompt_append: Optional[StagedPrompt] = None
         # Bumped whenever a table or length may change; keys the device-table cache.
         self._version = 0
         self._table_cache: Dict[tuple, _DecodeBatch] = {}
@@ -321,6 +339,53 @@ class KVAllocator:
         self._sequences[request_id] = _SequenceCache(sequence.reservation, blocks, length)
         self._touch()
         self._assert_accounting()
+
+    @contextmanager
+    def append_prompt(self, request_id: RequestId, tokens: int) -> Iterator[StagedPrompt]:
+        """Stage an append of `tokens` positions whose K/V the caller writes itself, layer
+        by layer (the fused prefill path: RoPE writes each layer's rotated K and V straight
+        into the slots append would fill).
+
+        The checks are append's (src/pagedcore/kv_cache.py:137-157), run before anything is
+        staged; the new blocks are the ones append would take (the free-list tail), only
+        borrowed while staged. The append is published when the block exits normally with
+        all 22 layers recorded; any exception discards it (the borrowed blocks stay free;
+        their slots may be dirty, as after a failed append). Other mutations raise meanwhile.
+        """
+        self._check_mutation()
+        self._assert_accounting()
+        sequence = self._sequences[request_id]
+        if type(tokens) is not int or tokens < 1:
+            raise ValueError("a prompt append needs a positive integer token count")
+        length = sequence.length + tokens
+        if length > CONTEXT_LIMIT:
+            raise ValueError("KV cache must not exceed 2048 token positions")
+        required = (length + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+        if required > sequence.reservation.maximum_block_credits:
+            raise RuntimeError("KV append exceeds request reservation")
+        additional = required - len(sequence.blocks)
+        if additional > len(self._free_blocks):
+            raise RuntimeError("KV pool has insufficient free blocks")
+        new_blocks = tuple(reversed(self._free_blocks[-additional:])) if additional else ()
+        blocks = sequence.blocks + new_blocks
+        slots = _slot_mapping(blocks, sequence.length, tokens)
+        positions = np.arange(sequence.length, length, dtype=np.int64)
+        both = torch.from_numpy(np.stack([slots, positions])).to(self._pool.device)
+        staged = StagedPrompt(request_id, tokens, both[0], both[1])
+        self._prompt_append = staged
+        self._touch()
+        try:
+            yield staged
+            if staged.written_layers != LAYERS:
+                raise RuntimeError("prompt append must write every cache layer before committing")
+            if additional:
+                del self._free_blocks[-additional:]
+            self._block_owners.update((block, request_id) for block in new_blocks)
+            self._sequences[request_id] = _SequenceCache(sequence.reservation, blocks, length)
+            self._assert_accounting()
+        finally:
+            self._prompt_append = None
+            self._touch()
 
     @contextmanager
     def append_decode(self, request_ids: Tuple[RequestId, ...]) -> Iterator[None]:
@@ -714,6 +779,8 @@ class KVAllocator:
         self._check_worker()
         if self._decode_appends is not None:
             raise RuntimeError("KV mutation is not allowed during a staged decode append")
+        if self._prompt_append is not None:
+            raise RuntimeError("KV mutation is not allowed during a staged prompt append")
 
     def _check_worker(self) -> None:
         if current_thread() is not self._worker:

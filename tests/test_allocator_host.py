@@ -683,3 +683,76 @@ def test_randomized_operations_match_an_independent_model(blocks):
         lambda: _AllocatorMachine(blocks),
         settings=settings(max_examples=40, stateful_step_count=30, deadline=None, derandomize=True, database=None),
     )
+
+
+# --- staged prompt append (the fused prefill write path) ----------------------------------
+
+
+def _twin_allocators():
+    """Two allocators in the same state, one request 'p' with 5 cached tokens and a
+    blocker 'b' holding the block after it, so new blocks come from the free-list tail."""
+    allocators = []
+    for _ in range(2):
+        allocator = cpu_allocator(torch.zeros((22, 2, 8, 16, 4, 64), dtype=torch.float16))
+        allocator.create(KVReservation(RequestId("p"), 4))
+        allocator.append(RequestId("p"), *kv_values(5))
+        allocator.create(KVReservation(RequestId("b"), 1))
+        allocator.append(RequestId("b"), *kv_values(3))
+        allocators.append(allocator)
+    return allocators
+
+
+def test_staged_prompt_append_takes_the_blocks_append_would_and_publishes_after_all_layers():
+    staged_alloc, plain = _twin_allocators()
+    request = RequestId("p")
+    plain.append(request, *kv_values(30, start=7))
+    with staged_alloc.append_prompt(request, 30) as staged:
+        assert staged.tokens == 30
+        assert staged.positions.tolist() == list(range(5, 35))
+        # nothing published while staged; other mutations are refused
+        assert staged_alloc.cached_length(request) == 5
+        with pytest.raises(RuntimeError, match="staged prompt append"):
+            staged_alloc.release_all(RequestId("b"))
+        for layer in range(22):
+            staged.record_layer(layer)
+    assert staged_alloc.block_table(request) == plain.block_table(request)
+    assert staged_alloc.capacity() == plain.capacity()
+    table = plain.block_table(request)
+    expected = [table[p // 16] * 16 + p % 16 for p in range(5, 35)]
+    assert staged.slot_mapping.tolist() == expected
+
+
+def test_staged_prompt_append_discards_on_error_and_requires_every_layer():
+    allocator, _ = _twin_allocators()
+    request = RequestId("p")
+    counts, table, free = allocator.capacity(), allocator.block_table(request), list(allocator._free_blocks)
+    with pytest.raises(RuntimeError, match="injected"):
+        with allocator.append_prompt(request, 20) as staged:
+            staged.record_layer(0)
+            raise RuntimeError("injected")
+    with pytest.raises(RuntimeError, match="every cache layer"):
+        with allocator.append_prompt(request, 20) as staged:
+            for layer in range(21):
+                staged.record_layer(layer)
+    with pytest.raises(ValueError, match="once in order"):
+        with allocator.append_prompt(request, 20) as staged:
+            staged.record_layer(1)
+    assert allocator.capacity() == counts and allocator.block_table(request) == table
+    assert list(allocator._free_blocks) == free and allocator.cached_length(request) == 5
+    allocator.release_all(RequestId("b"))  # mutations work again after the staging ended
+
+
+@pytest.mark.parametrize(
+    "tokens,error,needle",
+    [(0, ValueError, "positive"), (2044, ValueError, "2048"), (60, RuntimeError, "reservation"), (2.0, ValueError, "positive")],
+)
+def test_staged_prompt_append_checks_before_staging(tokens, error, needle):
+    allocator, _ = _twin_allocators()
+    counts = allocator.capacity()
+    with pytest.raises(error, match=needle):
+        with allocator.append_prompt(RequestId("p"), tokens):
+            pass
+    assert allocator.capacity() == counts and allocator._prompt_append is None
+    with pytest.raises(KeyError):
+        with allocator.append_prompt(RequestId("unknown"), 3):
+            pass

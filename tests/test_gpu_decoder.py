@@ -420,3 +420,110 @@ def test_decode_graph_replays_equal_decode_paged(device):
         assert graphed.capacity() == eager.capacity()
         assert [graphed.cached_length(r) for r in order] == [eager.cached_length(r) for r in order]
         torch.randn(1000, device=device).sum().item()  # unrelated eager work between replays
+
+
+# ---------------------------------------------------------------------------------------
+# Prompt attention (pc_prefill_attention)
+# ---------------------------------------------------------------------------------------
+
+
+def _causal_fp64(query, key, value):
+    """FP64 causal GQA attention: query [T, 32, 64], key/value [T, 4, 64] -> [T, 32, 64]."""
+    q = query.double().cpu().transpose(0, 1)  # [32, T, 64]
+    k = key.double().cpu().repeat_interleave(8, dim=1).transpose(0, 1)
+    v = value.double().cpu().repeat_interleave(8, dim=1).transpose(0, 1)
+    scores = q @ k.transpose(1, 2) / 8
+    tokens = query.shape[0]
+    scores = scores.masked_fill(~torch.ones(tokens, tokens, dtype=torch.bool).tril(), float("-inf"))
+    return (scores.softmax(-1) @ v).transpose(0, 1)
+
+
+@pytest.mark.parametrize("tokens", [1, 15, 16, 17, 100, 333, 2048])
+def test_prefill_attention_matches_fp32_and_fp64(device, tokens):
+    """Against the reference's fp32 dense attention (dense.py:91-99, causal) and FP64, both
+    within 2e-3; positions past the prompt are never written."""
+    gen = torch.Generator(device=device).manual_seed(tokens)
+    query = torch.randn(tokens, 32, 64, dtype=torch.float16, device=device, generator=gen)
+    key = torch.randn(tokens, 4, 64, dtype=torch.float16, device=device, generator=gen)
+    value = torch.randn(tokens, 4, 64, dtype=torch.float16, device=device, generator=gen)
+    out = torch.full((tokens + 16, 32, 64), 7.0, dtype=torch.float16, device=device)
+    _hip.prefill_attention(out[:tokens], query, key, value)
+    torch.cuda.synchronize()
+    got = out[:tokens].cpu()
+    assert torch.all(out[tokens:].cpu() == 7.0)
+    allowed = torch.ones(tokens, tokens, dtype=torch.bool).tril()[None, None]
+    expected = dref.dense_attention_fp32(
+        query.cpu().transpose(0, 1)[None], key.cpu().transpose(0, 1)[None], value.cpu().transpose(0, 1)[None], allowed
+    )[0].transpose(0, 1)
+    torch.testing.assert_close(got, expected, atol=2e-3, rtol=2e-3)
+    torch.testing.assert_close(got.double(), _causal_fp64(query, key, value), atol=2e-3, rtol=2e-3)
+
+
+def test_prefill_attention_sharp_and_known_answers(device):
+    """Scores of +-1000 scale (the running max must follow them exactly), V = c gives c, and
+    position 0 returns v[0] (one visible key)."""
+    gen = torch.Generator(device=device).manual_seed(9)
+    tokens = 70
+    query = (torch.randn(tokens, 32, 64, device=device, generator=gen) * 30).half()
+    key = (torch.randn(tokens, 4, 64, device=device, generator=gen) * 30).half()
+    value = torch.randn(tokens, 4, 64, dtype=torch.float16, device=device, generator=gen)
+    out = torch.empty(tokens, 32, 64, dtype=torch.float16, device=device)
+    _hip.prefill_attention(out, query, key, value)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out.cpu().double(), _causal_fp64(query, key, value), atol=2e-3, rtol=2e-3)
+    torch.testing.assert_close(out[0].cpu(), value[0].cpu().repeat_interleave(8, dim=0), atol=0, rtol=0)
+    constant = torch.full_like(value, 0.375)
+    _hip.prefill_attention(out, query, key, constant)
+    torch.cuda.synchronize()
+    assert torch.all(out.cpu() == 0.375)
+
+
+def test_prefill_attention_rejects_bad_arguments(device):
+    lib = _hip.load()
+    buf = torch.empty(64, dtype=torch.float16, device=device)
+    assert lib.pc_prefill_attention(buf.data_ptr(), buf.data_ptr(), buf.data_ptr(), buf.data_ptr(), -1, None) == 1
+    assert b"tokens" in lib.pc_last_error()
+    assert lib.pc_prefill_attention(buf.data_ptr() + 2, buf.data_ptr(), buf.data_ptr(), buf.data_ptr(), 1, None) == 1
+    assert b"aligned" in lib.pc_last_error()
+    assert lib.pc_prefill_attention(None, None, None, None, 0, None) == 0
+
+
+def test_prefill_paged_failure_publishes_nothing_and_allows_retry(device, monkeypatch):
+    """A failure inside the prefill forward (here: the prompt attention of layer 5) leaves
+    the request empty and the counts unchanged; the slots it wrote belong to free blocks
+    only, and a retry publishes the same table as an undisturbed prefill."""
+    weights = _synthetic(device)
+    pools = [torch.full((22, 2, 10, 16, 4, 64), float("nan"), dtype=torch.float16, device=device) for _ in range(2)]
+    failing, clean = (KVAllocator(pool) for pool in pools)
+    ids = (torch.arange(40)[None] % 31).to(device)
+    for allocator in (failing, clean):
+        allocator.create(KVReservation(RequestId("p"), 3))
+        allocator.create(KVReservation(RequestId("other"), 1))
+        dec.prefill_paged(ids[:, :9], weights, allocator, RequestId("other"))
+    counts = failing.capacity()
+    other = pools[0][:, :, failing.block_table(RequestId("other"))[0]].clone()
+    calls = 0
+    original = _hip.prefill_attention
+
+    def fail_at_layer_five(*args):
+        nonlocal calls
+        calls += 1
+        if calls == 6:
+            raise RuntimeError("injected prefill failure")
+        return original(*args)
+
+    monkeypatch.setattr(_hip, "prefill_attention", fail_at_layer_five)
+    with pytest.raises(RuntimeError, match="injected"):
+        dec.prefill_paged(ids, weights, failing, RequestId("p"))
+    monkeypatch.setattr(_hip, "prefill_attention", original)
+    assert failing.capacity() == counts
+    assert failing.cached_length(RequestId("p")) == 0 and failing.block_table(RequestId("p")) == ()
+    assert torch.equal(pools[0][:, :, failing.block_table(RequestId("other"))[0]].view(torch.int16), other.view(torch.int16))
+    retried = dec.prefill_paged(ids, weights, failing, RequestId("p"))
+    expected = dec.prefill_paged(ids, weights, clean, RequestId("p"))
+    assert torch.equal(retried, expected)
+    assert failing.block_table(RequestId("p")) == clean.block_table(RequestId("p"))
+    for logical in range(3):
+        for a_kv, b_kv in zip(failing.read_block(RequestId("p"), logical), clean.read_block(RequestId("p"), logical)):
+            assert torch.equal(a_kv.view(torch.int16), b_kv.view(torch.int16))
