@@ -328,6 +328,51 @@ def run_prefill(steps: int) -> dict:
     }
 
 
+def run_serving(requests: int = 128, max_active: int = 64) -> dict:
+    """Continuous batching through DecodeWorker on the full TinyLlama-architecture model:
+    `requests` prompts of U{128..1024} tokens, 64 new tokens each (ignore_eos, so every
+    request runs to its length), at most `max_active` active, one admission (prefill) per
+    iteration, FIFO; decode steps with a full batch replay a DecodeGraph. Timed from the
+    first iteration until the queue drains."""
+    from pagedcore_amd import decoder as dec
+    from pagedcore_amd.engine_types import RequestId
+    from pagedcore_amd.kv_cache import KVAllocator
+    from pagedcore_amd.worker import DecodeWorker, GenerationRequest
+
+    device = torch.device("cuda:0")
+    rng = workloads.rng(20261207)
+    weights = dec.random_weights(device=device, seed=20261207)
+    lengths = rng.integers(128, 1025, size=requests)
+    new_tokens = 64
+    blocks = max_active * -(-(1024 + new_tokens) // 16) + 64
+    allocator = KVAllocator(torch.empty((LAYERS, 2, blocks, 16, 4, 64), dtype=torch.float16, device=device))
+    worker = DecodeWorker(weights, allocator, max_active=max_active, graph_batch=max_active)
+    for index, length in enumerate(lengths):
+        prompt = tuple(int(t) for t in rng.integers(3, 32000, size=int(length)))
+        worker.submit(GenerationRequest(RequestId(f"req{index}"), prompt, new_tokens, ignore_eos=True))
+    iterations, emitted, batch_sum = 0, 0, 0
+    torch.cuda.synchronize(device)
+    start = time.perf_counter()
+    while not worker.idle:
+        emitted += len(worker.step())
+        batch_sum += sum(1 for _ in worker.active_ids)
+        iterations += 1
+    torch.cuda.synchronize(device)
+    seconds = time.perf_counter() - start
+    results = worker.results
+    assert len(results) == requests and all(len(r.greedy_ids) == new_tokens for r in results.values())
+    return {
+        "workload": f"continuous batching: {requests} requests, prompts U{{128..1024}}, {new_tokens} new tokens each, "
+        f"max {max_active} active, TinyLlama-architecture random weights; one prefill per iteration, full-batch "
+        "decode steps replay a DecodeGraph (captured during the run, included in the time)",
+        "seconds": round(seconds, 3),
+        "generated_tokens_per_s": round(requests * new_tokens / seconds, 1),
+        "prompt_tokens": int(lengths.sum()),
+        "iterations": iterations,
+        "mean_active": round(batch_sum / iterations, 2),
+    }
+
+
 def run_decode_step(steps: int, warmup: int) -> dict:
     """Full TinyLlama-architecture greedy decode step, batch 128, random N(0, 0.02) fp16
     weights, contexts uniform in 256..(2048 - steps - warmup - 1) pre-filled with N(0, 1)
@@ -497,6 +542,10 @@ def run_extra(selected: set, steps: int) -> dict:
         extra["prefill_2048"] = run_prefill(5)
         torch.cuda.empty_cache()
         print(f"prefill: {extra['prefill_2048']}", file=sys.stderr, flush=True)
+    if "serving" in selected:
+        extra["serving"] = run_serving()
+        torch.cuda.empty_cache()
+        print(f"serving: {extra['serving']}", file=sys.stderr, flush=True)
     if "decode_step" in selected:
         extra["decode_step_b128"] = run_decode_step(max(10, steps // 2), 3)
         torch.cuda.empty_cache()
@@ -515,7 +564,8 @@ def main() -> int:
     parser.add_argument("--workloads", default="attention,prompt_append,long_context,prefill,decode_step",
                         help="comma list: attention (the headline; without it only the others run, as a diagnostic line), prompt_append (2048-token prompt into a "
                         "fragmented pool), long_context (batch 256 x 2048, append + attention), prefill (one 2048-token "
-                        "prompt through the model), decode_step (full TinyLlama-architecture step, batch 128)")
+                        "prompt through the model), decode_step (full TinyLlama-architecture step, batch 128), serving "
+                        "(continuous batching of 128 requests; not in the default run)")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="run one plain copy of this many MiB first (counter calibration under rocprofv3 --pmc)")
     args = parser.parse_args()
@@ -531,7 +581,7 @@ def main() -> int:
     if args.calibrate_copy_mib > 0:
         calibration_copy(args.calibrate_copy_mib, torch.device("cuda:0"))
     selected = {name.strip() for name in args.workloads.split(",")}
-    unknown = selected - {"attention", "prompt_append", "long_context", "prefill", "decode_step"}
+    unknown = selected - {"attention", "prompt_append", "long_context", "prefill", "decode_step", "serving"}
     if unknown:
         print(f"unknown workloads {sorted(unknown)}", file=sys.stderr)
         return 2

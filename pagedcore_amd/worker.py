@@ -1,0 +1,249 @@
+"""Continuous-batching greedy decode worker over the paged KV path.
+
+The reference plans this loop but does not build it (its docs/DESIGN.md:348-357, "Scheduler
+iteration"); its single-request greedy semantics are src/pagedcore/decoder.py:61-100
+(GreedyResult, generate). One call of DecodeWorker.step is one iteration of that plan:
+
+  1. clean up: release the KV blocks, credits and active slot of requests that finished
+     (or were cancelled) in the previous iteration; drop cancelled requests still waiting;
+  2. admit at most one request, strictly first-in first-out: if an active slot is free and
+     the request's KV credits fit the unreserved pool, reserve, prefill (prefill_paged)
+     and select its first token; otherwise it keeps waiting (head-of-line blocking, as
+     planned);
+  3. decode: every active unfinished request, the newly admitted one included, in one
+     batched decode step (decode_paged, or a captured DecodeGraph when the batch has the
+     captured size);
+  4. emit: each request selects at most one token per iteration. A selected EOS stops the
+     request (unless ignore_eos) and is excluded from the emitted ids; reaching
+     max_new_tokens stops it with reason LENGTH, EOS taking precedence at the limit.
+
+Everything runs on the allocator's worker thread and stream, so a release is ordered after
+every launch that read the released blocks (the reference's stream-ordered reuse rule,
+docs/DESIGN.md:282).
+"""
+
+from __future__ import annotations
+
+from collections import deque
+from dataclasses import dataclass, field
+from enum import Enum
+from typing import Callable, Deque, Dict, List, Optional, Sequence, Tuple
+
+import torch
+from torch import Tensor
+
+from pagedcore_amd.engine_types import KVReservation, RequestId
+from pagedcore_amd.kv_cache import BLOCK_TOKENS, CONTEXT_LIMIT, KVAllocator
+
+EOS_TOKEN_ID = 2
+MAX_NEW_TOKENS = 256  # reference src/pagedcore/config.py:31 (and generate's bound, decoder.py:79)
+
+
+class FinishReason(str, Enum):
+    """Why a request stopped (reference src/pagedcore/engine_types.py:63-65)."""
+
+    EOS = "eos"
+    LENGTH = "length"
+
+
+@dataclass(frozen=True)
+class GenerationRequest:
+    """A prompt to complete greedily: up to max_new_tokens selected tokens."""
+
+    request_id: RequestId
+    input_ids: Tuple[int, ...]
+    max_new_tokens: int = 128
+    ignore_eos: bool = False
+
+    def __post_init__(self) -> None:
+        if not self.input_ids or any(type(t) is not int or t < 0 for t in self.input_ids):
+            raise ValueError("input_ids must be a nonempty sequence of token ids")
+        if type(self.max_new_tokens) is not int or not 1 <= self.max_new_tokens <= MAX_NEW_TOKENS:
+            raise ValueError("max_new_tokens must be an integer from 1 to 256")
+        if type(self.ignore_eos) is not bool:
+            raise ValueError("ignore_eos must be a boolean")
+        if len(self.input_ids) + self.max_new_tokens > CONTEXT_LIMIT:
+            raise ValueError("prompt tokens plus requested output must not exceed 2048")
+
+    @property
+    def block_credits(self) -> int:
+        """KV blocks the request can ever own: its prompt and every token it may decode."""
+        return -(-(len(self.input_ids) + self.max_new_tokens) // BLOCK_TOKENS)
+
+
+@dataclass(frozen=True)
+class GreedyResult:
+    """Selected ids; a stopping EOS is selected but excluded from emitted ids
+    (reference src/pagedcore/decoder.py:61-67)."""
+
+    greedy_ids: Tuple[int, ...]
+    emitted_ids: Tuple[int, ...]
+    finish_reason: FinishReason
+
+
+@dataclass
+class _Active:
+    request: GenerationRequest
+    selected: List[int] = field(default_factory=list)
+    finish: Optional[FinishReason] = None
+
+
+PrefillFn = Callable[[Tensor, object, KVAllocator, RequestId], Tensor]
+DecodeFn = Callable[[Tensor, object, KVAllocator, Tuple[RequestId, ...]], Tensor]
+
+
+class DecodeWorker:
+    """The scheduler iteration of the module docstring over one allocator and model.
+
+    `prefill` and `decode` default to the paged model (prefill_paged, decode_paged); tests
+    substitute them. With `graph_batch` set, decode steps whose batch has exactly that many
+    requests replay a DecodeGraph captured on first use (the saturated steady state of a
+    loaded server); other sizes run decode_paged.
+    """
+
+    def __init__(
+        self,
+        weights: object,
+        allocator: KVAllocator,
+        *,
+        max_active: int = 32,
+        eos_token_id: int = EOS_TOKEN_ID,
+        prefill: Optional[PrefillFn] = None,
+        decode: Optional[DecodeFn] = None,
+        graph_batch: Optional[int] = None,
+    ) -> None:
+        if type(max_active) is not int or max_active < 1:
+            raise ValueError("max_active must be a positive integer")
+        if prefill is None or decode is None:
+            from pagedcore_amd import decoder
+
+            prefill = prefill or decoder.prefill_paged
+            decode = decode or decoder.decode_paged
+        self._weights = weights
+        self._allocator = allocator
+        self._max_active = max_active
+        self._eos = eos_token_id
+        self._prefill = prefill
+        self._decode = decode
+        self._graph_batch = graph_batch
+        self._graph = None
+        self._pending: Deque[GenerationRequest] = deque()
+        self._active: Dict[RequestId, _Active] = {}
+        self._cancelled: set = set()
+        self._results: Dict[RequestId, GreedyResult] = {}
+        self._known: set = set()
+
+    # -- queue -----------------------------------------------------------------------------
+
+    def submit(self, request: GenerationRequest) -> None:
+        if request.request_id in self._known:
+            raise ValueError("request IDs must be unique")
+        if request.block_credits > self._allocator.pool.shape[2]:
+            raise ValueError("request exceeds total KV pool capacity")
+        self._known.add(request.request_id)
+        self._pending.append(request)
+
+    def cancel(self, request_id: RequestId) -> None:
+        """Stop a waiting or active request; its resources go at the next cleanup."""
+        if request_id not in self._known:
+            raise KeyError(request_id)
+        self._cancelled.add(request_id)
+
+    @property
+    def idle(self) -> bool:
+        return not self._pending and not self._active
+
+    @property
+    def active_ids(self) -> Tuple[RequestId, ...]:
+        return tuple(self._active)
+
+    @property
+    def pending_ids(self) -> Tuple[RequestId, ...]:
+        return tuple(r.request_id for r in self._pending)
+
+    @property
+    def results(self) -> Dict[RequestId, GreedyResult]:
+        return dict(self._results)
+
+    # -- one iteration -----------------------------------------------------------------------
+
+    def step(self) -> List[Tuple[RequestId, int]]:
+        """Run one scheduler iteration; returns the (request, token) pairs emitted."""
+        self._cleanup()
+        emitted: List[Tuple[RequestId, int]] = []
+        self._admit_one(emitted)
+        batch = tuple(rid for rid, state in self._active.items() if state.finish is None)
+        if batch:
+            tokens = torch.tensor(
+                [[self._active[rid].selected[-1]] for rid in batch], dtype=torch.int64, device=self._device()
+            )
+            logits = self._decode_batch(tokens, batch)
+            chosen = logits[:, -1].argmax(dim=-1).tolist()
+            for rid, token in zip(batch, chosen):
+                self._select(rid, int(token), emitted)
+        return emitted
+
+    def run(self, max_steps: Optional[int] = None) -> Dict[RequestId, GreedyResult]:
+        """Iterate until every submitted request finished (and was cleaned up)."""
+        steps = 0
+        while not self.idle:
+            if max_steps is not None and steps >= max_steps:
+                raise RuntimeError("worker did not drain within max_steps")
+            self.step()
+            steps += 1
+        return self.results
+
+    # -- internals --------------------------------------------------------------------------
+
+    def _device(self) -> torch.device:
+        return self._allocator.pool.device
+
+    def _cleanup(self) -> None:
+        for rid in [rid for rid, state in self._active.items() if state.finish is not None or rid in self._cancelled]:
+            state = self._active.pop(rid)
+            self._allocator.release_all(rid)
+            if state.finish is not None:
+                self._results[rid] = self._result(state)
+        if self._cancelled:
+            self._pending = deque(r for r in self._pending if r.request_id not in self._cancelled)
+
+    def _admit_one(self, emitted: List[Tuple[RequestId, int]]) -> None:
+        if not self._pending or len(self._active) >= self._max_active:
+            return
+        request = self._pending[0]
+        counts = self._allocator.capacity()
+        if request.block_credits > counts.total_blocks - counts.reserved_blocks:
+            return  # waits (strict FIFO: nothing behind it is admitted first)
+        self._pending.popleft()
+        rid = request.request_id
+        self._allocator.create(KVReservation(rid, request.block_credits))
+        self._active[rid] = _Active(request)
+        ids = torch.tensor([list(request.input_ids)], dtype=torch.int64, device=self._device())
+        logits = self._prefill(ids, self._weights, self._allocator, rid)
+        self._select(rid, int(logits[0, -1].argmax()), emitted)
+
+    def _decode_batch(self, tokens: Tensor, batch: Tuple[RequestId, ...]) -> Tensor:
+        if self._graph_batch is not None and len(batch) == self._graph_batch:
+            if self._graph is None:
+                from pagedcore_amd.decoder import DecodeGraph
+
+                self._graph = DecodeGraph(self._weights, self._allocator, self._graph_batch)
+            return self._graph.step(tokens, batch)
+        return self._decode(tokens, self._weights, self._allocator, batch)
+
+    def _select(self, rid: RequestId, token: int, emitted: List[Tuple[RequestId, int]]) -> None:
+        state = self._active[rid]
+        state.selected.append(token)
+        request = state.request
+        if token == self._eos and not request.ignore_eos:
+            state.finish = FinishReason.EOS  # selected, never emitted
+        else:
+            emitted.append((rid, token))
+            if len(state.selected) == request.max_new_tokens:
+                state.finish = FinishReason.LENGTH
+
+    @staticmethod
+    def _result(state: _Active) -> GreedyResult:
+        ids = tuple(state.selected)
+        emitted = ids[:-1] if state.finish is FinishReason.EOS else ids
+        return GreedyResult(ids, emitted, state.finish)

@@ -527,3 +527,48 @@ def test_prefill_paged_failure_publishes_nothing_and_allows_retry(device, monkey
     for logical in range(3):
         for a_kv, b_kv in zip(failing.read_block(RequestId("p"), logical), clean.read_block(RequestId("p"), logical)):
             assert torch.equal(a_kv.view(torch.int16), b_kv.view(torch.int16))
+
+
+def _generate_alone(weights, request, device):
+    """Greedy generation of one request by itself: prefill_paged, then decode_paged one
+    token at a time (the single-request loop of reference src/pagedcore/decoder.py:88-100)."""
+    from pagedcore_amd.worker import FinishReason
+
+    pool = torch.full((22, 2, 24, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    allocator.create(KVReservation(request.request_id, request.block_credits))
+    logits = dec.prefill_paged(torch.tensor([list(request.input_ids)], device=device), weights, allocator, request.request_id)
+    selected = [int(logits[0, -1].argmax())]
+    while True:
+        if selected[-1] == 2 and not request.ignore_eos:
+            return tuple(selected), FinishReason.EOS
+        if len(selected) == request.max_new_tokens:
+            return tuple(selected), FinishReason.LENGTH
+        logits = dec.decode_paged(torch.tensor([[selected[-1]]], device=device), weights, allocator, (request.request_id,))
+        selected.append(int(logits[0, -1].argmax()))
+
+
+@pytest.mark.parametrize("graph_batch", [None, 3])
+def test_worker_streams_equal_each_request_generated_alone(device, graph_batch):
+    """Continuous batching (requests joining and leaving the decode batch every few steps)
+    gives every request exactly the tokens it gets when generated by itself."""
+    from pagedcore_amd.worker import DecodeWorker, GenerationRequest
+
+    weights = _synthetic(device)
+    pool = torch.full((22, 2, 48, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    worker = DecodeWorker(weights, allocator, max_active=3, graph_batch=graph_batch)
+    gen = torch.Generator().manual_seed(13)
+    requests = []
+    for index in range(7):
+        prompt = tuple(int(t) for t in torch.randint(3, 31, (int(torch.randint(1, 40, (1,), generator=gen)),), generator=gen))
+        requests.append(GenerationRequest(RequestId(f"w{index}"), prompt, int(torch.randint(1, 12, (1,), generator=gen)),
+                                          ignore_eos=index % 2 == 0))
+        worker.submit(requests[-1])
+    results = worker.run(max_steps=500)
+    for request in requests:
+        ids, reason = _generate_alone(weights, request, device)
+        got = results[request.request_id]
+        assert got.greedy_ids == ids and got.finish_reason == reason, request.request_id
+    counts = allocator.capacity()
+    assert counts.owned_blocks == 0 and counts.reserved_blocks == 0 and counts.active_slots == 0

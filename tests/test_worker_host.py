@@ -1,0 +1,153 @@
+"""The continuous-batching worker's scheduling on the CPU (no GPU): FIFO admission under
+the active-slot and KV-credit limits, one token per request per iteration, EOS and length
+semantics (reference src/pagedcore/decoder.py:61-100), cleanup timing and cancellation.
+The model is replaced by scripted prefill/decode functions that keep the allocator's real
+bookkeeping (appends and staged decode writes through the CPU test writer)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from pagedcore_amd.engine_types import RequestId
+from pagedcore_amd.worker import DecodeWorker, FinishReason, GenerationRequest, GreedyResult
+from tests.support import cpu_allocator
+
+VOCAB = 40
+
+
+class ScriptedModel:
+    """Token chosen for request r at its n-th selection: script[r][n] (default 10 + n)."""
+
+    def __init__(self, script=None):
+        self.script = script or {}
+        self.decode_batches = []
+        self.prefills = []
+
+    def _logits(self, rid, n):
+        token = self.script.get(rid, {}).get(n, 10 + n)
+        logits = torch.zeros(VOCAB)
+        logits[token] = 1.0
+        return logits
+
+    def prefill(self, ids, weights, allocator, rid):
+        tokens = ids.shape[1]
+        kv = torch.zeros(22, tokens, 4, 64, dtype=torch.float16)
+        allocator.append(rid, kv, kv)
+        self.prefills.append(rid)
+        return torch.stack([self._logits(rid, 0)] * tokens)[None]
+
+    def decode(self, tokens, weights, allocator, rids):
+        self.decode_batches.append(rids)
+        with allocator.append_decode(rids):
+            kv = torch.zeros(len(rids), 4, 64, dtype=torch.float16)
+            for layer in range(22):
+                allocator.write_decode_layers(rids, layer, kv, kv)
+            out = []
+            for rid in rids:
+                # staged length = prompt + tokens selected so far: this is selection number n
+                n = allocator._decode_appends[rid].sequence.length - len(self.prompts[rid])
+                out.append(self._logits(rid, n))
+        return torch.stack(out)[:, None]
+
+
+def _worker(model, blocks=32, max_active=2):
+    allocator = cpu_allocator(torch.zeros((22, 2, blocks, 16, 4, 64), dtype=torch.float16))
+    return DecodeWorker(None, allocator, max_active=max_active, prefill=model.prefill, decode=model.decode), allocator
+
+
+def _request(name, prompt=5, new=4, **kw):
+    return GenerationRequest(RequestId(name), tuple(range(1, prompt + 1)), new, **kw)
+
+
+def _submit(worker, model, requests):
+    model.prompts = {r.request_id: r.input_ids for r in requests}
+    for r in requests:
+        worker.submit(r)
+
+
+def test_fifo_admission_one_per_iteration_and_active_limit():
+    model = ScriptedModel()
+    worker, allocator = _worker(model, max_active=2)
+    requests = [_request(f"r{i}", new=3) for i in range(4)]
+    _submit(worker, model, requests)
+    worker.step()
+    assert worker.active_ids == ("r0",) and model.decode_batches == [("r0",)]
+    worker.step()  # r0 selects its 3rd token and finishes; the active limit holds r2
+    assert worker.active_ids == ("r0", "r1") and model.decode_batches[-1] == ("r0", "r1")
+    assert worker.pending_ids == ("r2", "r3") and "r0" not in worker.results
+    worker.step()  # cleanup frees r0's slot first, then r2 is admitted
+    assert worker.active_ids == ("r1", "r2") and worker.pending_ids == ("r3",)
+    assert worker.results["r0"].greedy_ids == (10, 11, 12)
+    results = worker.run(max_steps=50)
+    assert model.prefills == ["r0", "r1", "r2", "r3"]
+    for r in requests:
+        assert results[r.request_id] == GreedyResult((10, 11, 12), (10, 11, 12), FinishReason.LENGTH)
+    assert allocator.capacity().owned_blocks == 0 and allocator.capacity().reserved_blocks == 0
+
+
+def test_each_request_selects_one_token_per_iteration_and_finishes_at_its_length():
+    model = ScriptedModel()
+    worker, _ = _worker(model, max_active=4)
+    _submit(worker, model, [_request("a", new=1), _request("b", new=2)])
+    emitted = worker.step()
+    assert emitted == [("a", 10)]  # a's only token comes from prefill; it is not decoded
+    assert model.decode_batches == []
+    emitted = worker.step()  # a cleaned up; b prefilled and decoded in the same iteration
+    assert emitted == [("b", 10), ("b", 11)]
+    assert model.decode_batches == [("b",)]
+    results = worker.run()
+    assert results["a"].greedy_ids == (10,) and results["b"].greedy_ids == (10, 11)
+
+
+def test_eos_is_selected_but_not_emitted_and_wins_at_the_limit():
+    model = ScriptedModel({RequestId("stop"): {2: 2}, RequestId("limit"): {2: 2}, RequestId("keep"): {1: 2}})
+    worker, _ = _worker(model, max_active=3)
+    _submit(worker, model, [_request("stop", new=5), _request("limit", new=3), _request("keep", new=3, ignore_eos=True)])
+    results = worker.run()
+    assert results["stop"] == GreedyResult((10, 11, 2), (10, 11), FinishReason.EOS)
+    assert results["limit"] == GreedyResult((10, 11, 2), (10, 11), FinishReason.EOS)
+    assert results["keep"] == GreedyResult((10, 2, 12), (10, 2, 12), FinishReason.LENGTH)
+
+
+def test_kv_credits_block_the_queue_head_and_release_comes_at_the_next_cleanup():
+    model = ScriptedModel()
+    # 6 blocks; "big" needs 5 credits (70 tokens + 4), "small" needs 1
+    worker, allocator = _worker(model, blocks=6, max_active=4)
+    _submit(worker, model, [_request("first", prompt=20, new=4), _request("big", prompt=70, new=4), _request("small", prompt=3, new=2)])
+    worker.step()
+    assert worker.active_ids == ("first",)
+    worker.step()
+    # big does not fit beside first's 2 credits; small waits behind it (strict FIFO)
+    assert worker.pending_ids == ("big", "small")
+    steps = 0
+    while "first" not in worker.results:
+        worker.step()
+        steps += 1
+    assert worker.active_ids == ("big",) and allocator.capacity().reserved_blocks == 5
+    results = worker.run()
+    assert set(results) == {"first", "big", "small"}
+
+
+def test_cancellation_and_validation():
+    model = ScriptedModel()
+    worker, allocator = _worker(model, max_active=1)
+    _submit(worker, model, [_request("a", new=10), _request("b", new=10)])
+    worker.step()
+    worker.cancel(RequestId("b"))
+    worker.cancel(RequestId("a"))
+    worker.step()
+    assert worker.idle and worker.results == {}
+    assert allocator.capacity().owned_blocks == 0
+    with pytest.raises(KeyError):
+        worker.cancel(RequestId("unknown"))
+    with pytest.raises(ValueError, match="unique"):
+        worker.submit(_request("a"))
+    with pytest.raises(ValueError, match="total KV pool"):
+        worker.submit(GenerationRequest(RequestId("huge"), tuple(range(600)), 10))
+    with pytest.raises(ValueError, match="2048"):
+        GenerationRequest(RequestId("x"), tuple(range(2000)), 100)
+    with pytest.raises(ValueError, match="1 to 256"):
+        GenerationRequest(RequestId("x"), (1,), 0)
+    with pytest.raises(ValueError, match="nonempty"):
+        GenerationRequest(RequestId("x"), (), 5)
