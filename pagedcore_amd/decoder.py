@@ -305,9 +305,14 @@ class DecodeGraph:
     allocator's staged-append bookkeeping, builds the plan into a pinned buffer, uploads
     it with two asynchronous copies and replays the graph; nothing synchronizes.
 
-    Same results, checks, errors and staged-append semantics as decode_paged for a batch
-    of `batch` requests (any requests, in any order, step to step); the kernels and their
-    shapes are the same, so the logits and cache bytes equal decode_paged's.
+    Same checks, errors and staged-append semantics as decode_paged for any 1 to `batch`
+    requests (any requests, in any order, step to step). A batch of exactly `batch`
+    requests runs the kernels decode_paged runs, at the same shapes, so its logits and
+    cache bytes equal decode_paged's. A smaller batch is padded to `batch` rows: a padding
+    row has no slot (it writes nothing to the pool) and context length 0 (no attention
+    work, its output row is never written), and its logits are dropped. The GEMMs then run
+    at `batch` rows, so the real rows' results may differ from decode_paged's at the
+    smaller row count in the last bits, as between any two GEMM shapes.
     """
 
     def __init__(self, weights: TinyLlamaWeights, allocator: KVAllocator, batch: int) -> None:
@@ -384,15 +389,16 @@ class DecodeGraph:
 
     @torch.inference_mode()
     def step(self, input_ids: Tensor, request_ids: Tuple[RequestId, ...]) -> Tensor:
-        """decode_paged(input_ids, weights, allocator, request_ids) by graph replay; the
-        batch must have the captured size. Returns fresh fp16 logits [B, 1, vocab]."""
+        """decode_paged(input_ids, weights, allocator, request_ids) by graph replay, for 1 to
+        `batch` requests. Returns fresh fp16 logits [len(request_ids), 1, vocab]."""
         request_ids = tuple(request_ids)
         if input_ids.dtype != torch.int64 or input_ids.ndim != 2 or input_ids.shape != (len(request_ids), 1):
             raise ValueError("input_ids must be int64 [batch, 1] matching request IDs")
         if input_ids.device != self._weights.embedding.device:
             raise ValueError("input_ids and weights must be on the same device")
-        if len(request_ids) != self.batch:
-            raise ValueError(f"this decode graph runs batches of {self.batch} requests")
+        rows = len(request_ids)
+        if not 1 <= rows <= self.batch:
+            raise ValueError(f"this decode graph runs batches of 1 to {self.batch} requests")
         allocator = self._allocator
         for request_id in request_ids:
             allocator.cached_length(request_id)  # KeyError for an unknown request
@@ -405,19 +411,22 @@ class DecodeGraph:
             host64, host32 = self._host[turn]
             h64 = host64.numpy()
             h32 = host32.numpy()
-            h64[1] = staged.slots
-            h64[2] = staged.positions
-            h32[: self.batch] = staged.lengths
+            h64[1, :rows] = staged.slots
+            h64[1, rows:] = -1  # padding rows: no slot, position 0, context length 0
+            h64[2, :rows] = staged.positions
+            h64[2, rows:] = 0
+            h32[:rows] = staged.lengths
+            h32[rows : self.batch] = 0
             _hip.decode_plan_into(staged.lengths, staged.tables, h32[self._lens_span :].reshape(self._capacity, -1))
             self._inputs64[1:].copy_(host64[1:], non_blocking=True)
             self._inputs32.copy_(host32, non_blocking=True)
             uploaded = torch.cuda.Event()
             uploaded.record()
             self._uploaded[turn] = uploaded
-            self._inputs64[0].copy_(input_ids[:, 0])
+            self._inputs64[0, :rows].copy_(input_ids[:, 0])
             self._graph.replay()
             allocator.record_decode_writes(request_ids, LAYERS)
-            logits = self._logits.clone()
+            logits = self._logits[:rows].clone()
         return logits.unsqueeze(1)
 
 

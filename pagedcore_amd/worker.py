@@ -11,8 +11,8 @@ iteration"); its single-request greedy semantics are src/pagedcore/decoder.py:61
      and select its first token; otherwise it keeps waiting (head-of-line blocking, as
      planned);
   3. decode: every active unfinished request, the newly admitted one included, in one
-     batched decode step (decode_paged, or a captured DecodeGraph when the batch has the
-     captured size);
+     batched decode step (decode_paged, or the replay of a captured DecodeGraph of the
+     smallest configured size that holds the batch);
   4. emit: each request selects at most one token per iteration. A selected EOS stops the
      request (unless ignore_eos) and is excluded from the emitted ids; reaching
      max_new_tokens stops it with reason LENGTH, EOS taking precedence at the limit.
@@ -27,7 +27,7 @@ from __future__ import annotations
 from collections import deque
 from dataclasses import dataclass, field
 from enum import Enum
-from typing import Callable, Deque, Dict, List, Optional, Sequence, Tuple
+from typing import Callable, Deque, Dict, List, Optional, Sequence, Tuple, Union
 
 import torch
 from torch import Tensor
@@ -96,9 +96,11 @@ class DecodeWorker:
     """The scheduler iteration of the module docstring over one allocator and model.
 
     `prefill` and `decode` default to the paged model (prefill_paged, decode_paged); tests
-    substitute them. With `graph_batch` set, decode steps whose batch has exactly that many
-    requests replay a DecodeGraph captured on first use (the saturated steady state of a
-    loaded server); other sizes run decode_paged.
+    substitute them. `graph_batch` (one size or several) names the batch sizes that get a
+    captured DecodeGraph: a decode step of n requests replays the graph of the smallest
+    such size >= n (padding rows write nothing and their logits are dropped), captured on
+    first use or all at once by capture_graphs(); a step larger than every size runs
+    decode_paged.
     """
 
     def __init__(
@@ -110,10 +112,13 @@ class DecodeWorker:
         eos_token_id: int = EOS_TOKEN_ID,
         prefill: Optional[PrefillFn] = None,
         decode: Optional[DecodeFn] = None,
-        graph_batch: Optional[int] = None,
+        graph_batch: Union[None, int, Sequence[int]] = None,
     ) -> None:
         if type(max_active) is not int or max_active < 1:
             raise ValueError("max_active must be a positive integer")
+        sizes = () if graph_batch is None else (graph_batch,) if isinstance(graph_batch, int) else tuple(graph_batch)
+        if any(type(size) is not int or size < 1 for size in sizes):
+            raise ValueError("graph batch sizes must be positive integers")
         if prefill is None or decode is None:
             from pagedcore_amd import decoder
 
@@ -125,8 +130,8 @@ class DecodeWorker:
         self._eos = eos_token_id
         self._prefill = prefill
         self._decode = decode
-        self._graph_batch = graph_batch
-        self._graph = None
+        self._graph_sizes = tuple(sorted(set(sizes)))
+        self._graphs: Dict[int, object] = {}
         self._pending: Deque[GenerationRequest] = deque()
         self._active: Dict[RequestId, _Active] = {}
         self._cancelled: set = set()
@@ -222,13 +227,24 @@ class DecodeWorker:
         logits = self._prefill(ids, self._weights, self._allocator, rid)
         self._select(rid, int(logits[0, -1].argmax()), emitted)
 
-    def _decode_batch(self, tokens: Tensor, batch: Tuple[RequestId, ...]) -> Tensor:
-        if self._graph_batch is not None and len(batch) == self._graph_batch:
-            if self._graph is None:
-                from pagedcore_amd.decoder import DecodeGraph
+    def _graph_for(self, size: int):
+        graph = self._graphs.get(size)
+        if graph is None:
+            from pagedcore_amd.decoder import DecodeGraph
 
-                self._graph = DecodeGraph(self._weights, self._allocator, self._graph_batch)
-            return self._graph.step(tokens, batch)
+            graph = self._graphs[size] = DecodeGraph(self._weights, self._allocator, size)
+        return graph
+
+    def capture_graphs(self) -> None:
+        """Capture the DecodeGraph of every configured batch size now (each capture runs
+        one eager step with no pool writes), instead of at its first use."""
+        for size in self._graph_sizes:
+            self._graph_for(size)
+
+    def _decode_batch(self, tokens: Tensor, batch: Tuple[RequestId, ...]) -> Tensor:
+        size = next((size for size in self._graph_sizes if size >= len(batch)), None)
+        if size is not None:
+            return self._graph_for(size).step(tokens, batch)
         return self._decode(tokens, self._weights, self._allocator, batch)
 
     def _select(self, rid: RequestId, token: int, emitted: List[Tuple[RequestId, int]]) -> None:

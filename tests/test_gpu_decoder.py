@@ -402,8 +402,8 @@ def test_decode_graph_replays_equal_decode_paged(device):
     for request, length in zip(requests, lengths):
         admit(request, length)
     graph = dec.DecodeGraph(weights, graphed, batch=len(lengths))
-    with pytest.raises(ValueError, match="batches of 7"):
-        graph.step(torch.zeros((2, 1), dtype=torch.int64, device=device), tuple(requests[:2]))
+    with pytest.raises(ValueError, match="batches of 1 to 7"):
+        graph.step(torch.zeros((8, 1), dtype=torch.int64, device=device), tuple(RequestId(f"x{i}") for i in range(8)))
     for step in range(5):
         if step == 3:  # replace a request between steps
             for allocator in (eager, graphed):
@@ -419,6 +419,47 @@ def test_decode_graph_replays_equal_decode_paged(device):
         assert torch.equal(pools[0].view(torch.int16), pools[1].view(torch.int16))
         assert graphed.capacity() == eager.capacity()
         assert [graphed.cached_length(r) for r in order] == [eager.cached_length(r) for r in order]
+        torch.randn(1000, device=device).sum().item()  # unrelated eager work between replays
+
+
+def test_decode_graph_pads_smaller_batches(device):
+    """A DecodeGraph of 6 rows stepping 1, 4, 6 and 3 requests against eager decode_paged on
+    a twin pool: the padding rows write nothing (every pool byte outside the real rows'
+    new slots, NaN poison included, stays identical) and the real rows' logits and new K/V
+    agree within the reference's tolerances (the GEMMs run at 6 rows instead of the batch
+    size), with the same greedy tokens and the same allocator state."""
+    weights = _synthetic(device)
+    lengths = (3, 16, 40, 77, 130, 200)
+    pools = [torch.full((22, 2, 80, 16, 4, 64), float("nan"), dtype=torch.float16, device=device) for _ in range(2)]
+    eager, graphed = (KVAllocator(pool) for pool in pools)
+    requests = [RequestId(f"p{row}") for row in range(len(lengths))]
+    for request, length in zip(requests, lengths):
+        ids = ((torch.arange(length)[None] * 7 + length) % 31).to(device)
+        for allocator in (eager, graphed):
+            allocator.create(KVReservation(request, (length + 4 + 15) // 16))
+            dec.prefill_paged(ids, weights, allocator, request)
+    graph = dec.DecodeGraph(weights, graphed, batch=6)
+    for step, rows in enumerate((1, 4, 6, 3)):
+        order = tuple(requests[(step + row) % 6] for row in range(rows))
+        tokens = torch.tensor([[(3 * step + row) % 31] for row in range(rows)], device=device)
+        before = pools[1].clone()
+        expected = dec.decode_paged(tokens, weights, eager, order)
+        got = graph.step(tokens, order)
+        torch.cuda.synchronize()
+        assert got.shape == expected.shape == (rows, 1, 31)
+        torch.testing.assert_close(got, expected, atol=5e-3, rtol=5e-3)
+        assert torch.equal(got.argmax(-1), expected.argmax(-1))
+        assert graphed.capacity() == eager.capacity()
+        written = torch.zeros(pools[1].shape[2:4], dtype=torch.bool, device=device)
+        for request in order:
+            length = graphed.cached_length(request)
+            assert length == eager.cached_length(request)
+            assert graphed.block_table(request) == eager.block_table(request)
+            block, slot = divmod(length - 1, 16)
+            written[graphed.block_table(request)[block], slot] = True
+        untouched = ~written
+        assert torch.equal(pools[1][:, :, untouched].view(torch.int16), before[:, :, untouched].view(torch.int16))
+        torch.testing.assert_close(pools[1][:, :, written], pools[0][:, :, written], atol=2e-3, rtol=2e-3)
         torch.randn(1000, device=device).sum().item()  # unrelated eager work between replays
 
 
@@ -548,7 +589,7 @@ def _generate_alone(weights, request, device):
         selected.append(int(logits[0, -1].argmax()))
 
 
-@pytest.mark.parametrize("graph_batch", [None, 3])
+@pytest.mark.parametrize("graph_batch", [None, 3, (2, 4)])
 def test_worker_streams_equal_each_request_generated_alone(device, graph_batch):
     """Continuous batching (requests joining and leaving the decode batch every few steps)
     gives every request exactly the tokens it gets when generated by itself."""

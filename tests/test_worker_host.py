@@ -151,3 +151,44 @@ def test_cancellation_and_validation():
         GenerationRequest(RequestId("x"), (1,), 0)
     with pytest.raises(ValueError, match="nonempty"):
         GenerationRequest(RequestId("x"), (), 5)
+
+
+def test_decode_steps_replay_the_smallest_graph_that_holds_the_batch(monkeypatch):
+    """With graph sizes (4, 2) a step of n requests replays the graph of the smallest size
+    >= n, captured once on first use; a step larger than every size runs decode_paged."""
+    from pagedcore_amd import decoder
+
+    model = ScriptedModel()
+    made, used = [], []
+
+    class RecordingGraph:
+        def __init__(self, weights, allocator, batch):
+            made.append(batch)
+            self.batch, self.allocator = batch, allocator
+
+        def step(self, tokens, rids):
+            assert len(rids) <= self.batch
+            used.append((self.batch, len(rids)))
+            return model.decode(tokens, None, self.allocator, rids)
+
+    monkeypatch.setattr(decoder, "DecodeGraph", RecordingGraph)
+    allocator = cpu_allocator(torch.zeros((22, 2, 32, 16, 4, 64), dtype=torch.float16))
+    worker = DecodeWorker(None, allocator, max_active=5, prefill=model.prefill, decode=model.decode, graph_batch=(4, 2))
+    _submit(worker, model, [_request(f"r{i}", new=8) for i in range(5)])
+    for _ in range(6):
+        worker.step()
+    # one admission per iteration: batches of 1, 2, 3, 4, 5, 5
+    assert used == [(2, 1), (2, 2), (4, 3), (4, 4)]
+    assert [len(batch) for batch in model.decode_batches] == [1, 2, 3, 4, 5, 5]
+    assert made == [2, 4]
+    worker.capture_graphs()
+    assert made == [2, 4]  # already captured
+    results = worker.run()
+    assert all(results[f"r{i}"].greedy_ids == tuple(range(10, 18)) for i in range(5))
+    captured = []
+    monkeypatch.setattr(decoder, "DecodeGraph", lambda weights, allocator, batch: captured.append(batch))
+    DecodeWorker(None, allocator, prefill=model.prefill, decode=model.decode, graph_batch=(8, 1, 8)).capture_graphs()
+    assert captured == [1, 8]
+    for bad in (0, (2, 0), True, (3.0,)):
+        with pytest.raises(ValueError, match="graph batch sizes"):
+            DecodeWorker(None, allocator, prefill=model.prefill, decode=model.decode, graph_batch=bad)
