@@ -334,8 +334,9 @@ def run_serving(requests: int = 128, max_active: int = 64) -> dict:
     request runs to its length), at most `max_active` active, one admission (prefill) per
     iteration, FIFO; every decode step replays one DecodeGraph of `max_active` rows (a
     smaller batch is padded: the step's GEMMs stream the same weights at any row count up
-    to 128, so padding costs little). The graph is captured before the timed region; timed
-    from the first iteration until the queue drains."""
+    to 128, so padding costs little), and every prefill replays the PrefillGraph of the
+    smallest multiple of 128 positions that holds the prompt. The graphs are captured
+    before the timed region; timed from the first iteration until the queue drains."""
     from pagedcore_amd import decoder as dec
     from pagedcore_amd.engine_types import RequestId
     from pagedcore_amd.kv_cache import KVAllocator
@@ -348,7 +349,8 @@ def run_serving(requests: int = 128, max_active: int = 64) -> dict:
     new_tokens = 64
     blocks = max_active * -(-(1024 + new_tokens) // 16) + 64
     allocator = KVAllocator(torch.empty((LAYERS, 2, blocks, 16, 4, 64), dtype=torch.float16, device=device))
-    worker = DecodeWorker(weights, allocator, max_active=max_active, graph_batch=max_active)
+    prompt_sizes = tuple(range(128, 1025, 128))
+    worker = DecodeWorker(weights, allocator, max_active=max_active, graph_batch=max_active, prefill_graph_tokens=prompt_sizes)
     worker.capture_graphs()  # at start-up, before the timed run
     for index, length in enumerate(lengths):
         prompt = tuple(int(t) for t in rng.integers(3, 32000, size=int(length)))
@@ -367,7 +369,8 @@ def run_serving(requests: int = 128, max_active: int = 64) -> dict:
     return {
         "workload": f"continuous batching: {requests} requests, prompts U{{128..1024}}, {new_tokens} new tokens each, "
         f"max {max_active} active, TinyLlama-architecture random weights; one prefill per iteration, every "
-        f"decode step replays a {max_active}-row DecodeGraph (padded when fewer are active; captured before timing)",
+        f"decode step replays a {max_active}-row DecodeGraph (padded when fewer are active), every prefill a PrefillGraph "
+        "of the smallest multiple of 128 positions holding the prompt (graphs captured before timing)",
         "seconds": round(seconds, 3),
         "generated_tokens_per_s": round(requests * new_tokens / seconds, 1),
         "prompt_tokens": int(lengths.sum()),

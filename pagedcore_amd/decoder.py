@@ -462,33 +462,122 @@ def prefill_paged(
     if tokens < 1 or tokens > CONTEXT_LIMIT:
         raise ValueError("forward requires 1 to 2048 total cached token positions")
     _check_gpu(allocator, weights, "prefill")
-    device = input_ids.device
-    table = rope_table(device)
-    pool = allocator.pool
+    table = rope_table(input_ids.device)
     with allocator.append_prompt(request_id, tokens) as staged:
-        hidden = F.embedding(input_ids[0], weights.embedding)  # [T, 2048]
-        x = torch.empty_like(hidden)
-        _hip.add_rms_norm(x, hidden, None, weights.layers[0].input_norm, RMS_EPS)
-        key = torch.empty((tokens, KV_HEADS, HEAD_DIM), dtype=torch.float16, device=device)
-        value = torch.empty_like(key)
-        query = torch.empty((tokens, Q_HEADS, HEAD_DIM), dtype=torch.float16, device=device)
-        attended = torch.empty_like(query)
-        for index, layer in enumerate(weights.layers):
-            fused = _fused(layer)
-            qkv = F.linear(x, fused.qkv)
-            _hip.rope_kv_append(
-                query, qkv, staged.positions, table, key_out=key, value_out=value, pool=pool, layer=index,
-                slot_mapping=staged.slot_mapping,
-            )
-            staged.record_layer(index)
-            _hip.prefill_attention(attended, query, key, value)
-            projected = F.linear(attended.view(tokens, HIDDEN), layer.o_proj)
-            _hip.add_rms_norm(x, hidden, projected, layer.post_attention_norm, RMS_EPS)
-            gate_up = F.linear(x, fused.gate_up)
-            activated = torch.empty((tokens, gate_up.shape[1] // 2), dtype=torch.float16, device=device)
-            _hip.silu_mul(activated, gate_up)
-            down = F.linear(activated, layer.down_proj)
-            following = weights.layers[index + 1].input_norm if index + 1 < LAYERS else weights.final_norm
-            _hip.add_rms_norm(x, hidden, down, following, RMS_EPS)
+        x = _prefill_forward(input_ids[0], staged.positions, staged.slot_mapping, weights, allocator.pool, table,
+                             staged.record_layer)
         logits = F.linear(x, weights.lm_head)
     return logits.unsqueeze(0)
+
+
+def _prefill_forward(ids: Tensor, positions: Tensor, slots: Tensor, weights: TinyLlamaWeights, pool: Tensor,
+                     table: Tensor, on_layer=None) -> Tensor:
+    """The prompt's forward over T = len(ids) rows: per layer, pc_rope_kv_append writes the
+    rotated K and the V to `slots` (negative: not written) and to the contiguous copies
+    the prompt's attention reads; returns the final-normed hidden states [T, 2048].
+    `on_layer(index)` runs after each layer's cache write is enqueued."""
+    tokens = ids.shape[0]
+    device = ids.device
+    hidden = F.embedding(ids, weights.embedding)  # [T, 2048]
+    x = torch.empty_like(hidden)
+    _hip.add_rms_norm(x, hidden, None, weights.layers[0].input_norm, RMS_EPS)
+    key = torch.empty((tokens, KV_HEADS, HEAD_DIM), dtype=torch.float16, device=device)
+    value = torch.empty_like(key)
+    query = torch.empty((tokens, Q_HEADS, HEAD_DIM), dtype=torch.float16, device=device)
+    attended = torch.empty_like(query)
+    for index, layer in enumerate(weights.layers):
+        fused = _fused(layer)
+        qkv = F.linear(x, fused.qkv)
+        _hip.rope_kv_append(query, qkv, positions, table, key_out=key, value_out=value, pool=pool, layer=index,
+                            slot_mapping=slots)
+        if on_layer is not None:
+            on_layer(index)
+        _hip.prefill_attention(attended, query, key, value)
+        projected = F.linear(attended.view(tokens, HIDDEN), layer.o_proj)
+        _hip.add_rms_norm(x, hidden, projected, layer.post_attention_norm, RMS_EPS)
+        gate_up = F.linear(x, fused.gate_up)
+        activated = torch.empty((tokens, gate_up.shape[1] // 2), dtype=torch.float16, device=device)
+        _hip.silu_mul(activated, gate_up)
+        down = F.linear(activated, layer.down_proj)
+        following = weights.layers[index + 1].input_norm if index + 1 < LAYERS else weights.final_norm
+        _hip.add_rms_norm(x, hidden, down, following, RMS_EPS)
+    return x
+
+
+class PrefillGraph:
+    """prefill_paged for prompts of 1 to `tokens` positions, captured once as a HIP graph
+    and replayed, returning only the logits of the prompt's last position (what greedy
+    generation selects from).
+
+    prefill_paged issues about 200 launches from Python (about 2.6 ms of host time at any
+    prompt length), so short prompts are host-bound. Here the forward is captured at
+    `tokens` rows over static inputs: token ids, slot mapping and the index of the last
+    real row (positions are 0 .. tokens - 1: the cache is empty). A shorter prompt is
+    padded at the end; causal attention keeps every real row blind to the padding rows
+    after it, and a padding row's slot is -1, so it writes nothing to the pool. Per call
+    the host stages the append (KVAllocator.append_prompt, same checks, errors and
+    publish-after-forward semantics as prefill_paged), copies the inputs into the static
+    buffers and replays the graph; nothing synchronizes.
+
+    The GEMMs run at `tokens` rows, and the LM head on the last row alone, so logits and
+    cache bytes may differ from prefill_paged's in the last bits, as between any two GEMM
+    shapes.
+    """
+
+    def __init__(self, weights: TinyLlamaWeights, allocator: KVAllocator, tokens: int) -> None:
+        _check_weights(weights, "prefill")
+        if type(tokens) is not int or not 1 <= tokens <= CONTEXT_LIMIT:
+            raise ValueError("a prefill graph holds 1 to 2048 prompt positions")
+        _check_gpu(allocator, weights, "prefill")
+        device = allocator.pool.device
+        self.tokens = tokens
+        self._weights = weights
+        self._allocator = allocator
+        self._table = rope_table(device)
+        # Static inputs: int64 [4, tokens] = token ids, slots, positions, and (row 3,
+        # element 0) the last real row's index.
+        self._inputs = torch.zeros((4, tokens), dtype=torch.int64, device=device)
+        self._inputs[1].fill_(-1)  # warm-up and capture write nothing to the pool
+        self._inputs[2].copy_(torch.arange(tokens, device=device))
+        self._inputs[3, 0] = tokens - 1
+        stream = torch.cuda.current_stream(device)
+        self._forward()  # eager warm-up: library initialisation and GEMM selection outside the capture
+        torch.cuda.synchronize(device)
+        self._graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(device=device)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side), torch.cuda.graph(self._graph, stream=side):
+            self._logits = self._forward()
+        stream.wait_stream(side)
+        torch.cuda.synchronize(device)
+
+    def _forward(self) -> Tensor:
+        ids, slots, positions, last = self._inputs
+        x = _prefill_forward(ids, positions, slots, self._weights, self._allocator.pool, self._table)
+        return F.linear(x.index_select(0, last[:1]), self._weights.lm_head)  # [1, vocab]
+
+    @torch.inference_mode()
+    def step(self, input_ids: Tensor, request_id: RequestId) -> Tensor:
+        """prefill_paged(input_ids, weights, allocator, request_id) by graph replay for a
+        prompt of 1 to `tokens` positions; returns fresh fp16 logits [1, 1, vocab] of the
+        prompt's last position."""
+        allocator = self._allocator
+        if allocator.cached_length(request_id) != 0:
+            raise ValueError("paged prefill requires an empty request cache")
+        if input_ids.dtype != torch.int64 or input_ids.ndim != 2 or input_ids.shape[0] != 1:
+            raise ValueError("input_ids must be int64 [1, tokens]")
+        if input_ids.device != self._weights.embedding.device:
+            raise ValueError("input_ids and weights must be on the same device")
+        rows = input_ids.shape[1]
+        if not 1 <= rows <= self.tokens:
+            raise ValueError(f"this prefill graph holds prompts of 1 to {self.tokens} positions")
+        with allocator.append_prompt(request_id, rows) as staged:
+            self._inputs[0, :rows].copy_(input_ids[0])
+            self._inputs[1, :rows].copy_(staged.slot_mapping)
+            self._inputs[1, rows:].fill_(-1)
+            self._inputs[3, :1].fill_(rows - 1)
+            self._graph.replay()
+            for index in range(LAYERS):
+                staged.record_layer(index)
+            logits = self._logits.clone()
+        return logits.unsqueeze(0)

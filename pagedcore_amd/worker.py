@@ -7,8 +7,8 @@ iteration"); its single-request greedy semantics are src/pagedcore/decoder.py:61
   1. clean up: release the KV blocks, credits and active slot of requests that finished
      (or were cancelled) in the previous iteration; drop cancelled requests still waiting;
   2. admit at most one request, strictly first-in first-out: if an active slot is free and
-     the request's KV credits fit the unreserved pool, reserve, prefill (prefill_paged)
-     and select its first token; otherwise it keeps waiting (head-of-line blocking, as
+     the request's KV credits fit the unreserved pool, reserve, prefill (prefill_paged,
+     or the replay of a captured PrefillGraph) and select its first token; otherwise it keeps waiting (head-of-line blocking, as
      planned);
   3. decode: every active unfinished request, the newly admitted one included, in one
      batched decode step (decode_paged, or the replay of a captured DecodeGraph of the
@@ -100,7 +100,9 @@ class DecodeWorker:
     captured DecodeGraph: a decode step of n requests replays the graph of the smallest
     such size >= n (padding rows write nothing and their logits are dropped), captured on
     first use or all at once by capture_graphs(); a step larger than every size runs
-    decode_paged.
+    decode_paged. `prefill_graph_tokens` does the same for admissions: a prompt of T
+    positions replays the PrefillGraph of the smallest size >= T (it computes the last
+    position's logits only, all the selection needs); longer prompts run prefill_paged.
     """
 
     def __init__(
@@ -113,12 +115,16 @@ class DecodeWorker:
         prefill: Optional[PrefillFn] = None,
         decode: Optional[DecodeFn] = None,
         graph_batch: Union[None, int, Sequence[int]] = None,
+        prefill_graph_tokens: Sequence[int] = (),
     ) -> None:
         if type(max_active) is not int or max_active < 1:
             raise ValueError("max_active must be a positive integer")
         sizes = () if graph_batch is None else (graph_batch,) if isinstance(graph_batch, int) else tuple(graph_batch)
         if any(type(size) is not int or size < 1 for size in sizes):
             raise ValueError("graph batch sizes must be positive integers")
+        prompt_sizes = tuple(prefill_graph_tokens)
+        if any(type(size) is not int or not 1 <= size <= CONTEXT_LIMIT for size in prompt_sizes):
+            raise ValueError("prefill graph sizes must be integers from 1 to 2048")
         if prefill is None or decode is None:
             from pagedcore_amd import decoder
 
@@ -132,6 +138,8 @@ class DecodeWorker:
         self._decode = decode
         self._graph_sizes = tuple(sorted(set(sizes)))
         self._graphs: Dict[int, object] = {}
+        self._prompt_sizes = tuple(sorted(set(prompt_sizes)))
+        self._prefill_graphs: Dict[int, object] = {}
         self._pending: Deque[GenerationRequest] = deque()
         self._active: Dict[RequestId, _Active] = {}
         self._cancelled: set = set()
@@ -224,7 +232,11 @@ class DecodeWorker:
         self._allocator.create(KVReservation(rid, request.block_credits))
         self._active[rid] = _Active(request)
         ids = torch.tensor([list(request.input_ids)], dtype=torch.int64, device=self._device())
-        logits = self._prefill(ids, self._weights, self._allocator, rid)
+        size = next((size for size in self._prompt_sizes if size >= len(request.input_ids)), None)
+        if size is not None:
+            logits = self._prefill_graph_for(size).step(ids, rid)
+        else:
+            logits = self._prefill(ids, self._weights, self._allocator, rid)
         self._select(rid, int(logits[0, -1].argmax()), emitted)
 
     def _graph_for(self, size: int):
@@ -235,11 +247,21 @@ class DecodeWorker:
             graph = self._graphs[size] = DecodeGraph(self._weights, self._allocator, size)
         return graph
 
+    def _prefill_graph_for(self, size: int):
+        graph = self._prefill_graphs.get(size)
+        if graph is None:
+            from pagedcore_amd.decoder import PrefillGraph
+
+            graph = self._prefill_graphs[size] = PrefillGraph(self._weights, self._allocator, size)
+        return graph
+
     def capture_graphs(self) -> None:
-        """Capture the DecodeGraph of every configured batch size now (each capture runs
-        one eager step with no pool writes), instead of at its first use."""
+        """Capture the DecodeGraph and PrefillGraph of every configured size now (each
+        capture runs one eager forward with no pool writes), instead of at first use."""
         for size in self._graph_sizes:
             self._graph_for(size)
+        for size in self._prompt_sizes:
+            self._prefill_graph_for(size)
 
     def _decode_batch(self, tokens: Tensor, batch: Tuple[RequestId, ...]) -> Tensor:
         size = next((size for size in self._graph_sizes if size >= len(batch)), None)

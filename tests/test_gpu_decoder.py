@@ -463,6 +463,63 @@ def test_decode_graph_pads_smaller_batches(device):
         torch.randn(1000, device=device).sum().item()  # unrelated eager work between replays
 
 
+def test_prefill_graph_matches_prefill_paged(device):
+    """A 128-position PrefillGraph against prefill_paged on a twin pool for prompts of 1, 16,
+    37, 100 and 128 positions: the same tables, lengths and counts, and every pool byte
+    outside the prompt's slots (NaN poison included) untouched. The last position's
+    logits and the cached K/V meet the bars prefill_paged's own test applies against the
+    oracle (its GEMMs run at 128 rows, so the two paths differ by rounding): logits within
+    5e-3, layer-0 K/V within 2e-3, every layer as accurate as the CPU fp16 forward
+    against fp32. Errors leave nothing staged."""
+    weights = _synthetic(device)
+    host_weights = _cpu(weights)
+    exact = _fp32(host_weights)
+    pools = [torch.full((22, 2, 40, 16, 4, 64), float("nan"), dtype=torch.float16, device=device) for _ in range(2)]
+    eager, graphed = (KVAllocator(pool) for pool in pools)
+    graph = dec.PrefillGraph(weights, graphed, 128)
+    for index, length in enumerate((1, 16, 37, 100, 128)):
+        request = RequestId(f"q{index}")
+        for allocator in (eager, graphed):
+            allocator.create(KVReservation(request, (length + 15) // 16))
+        ids = (torch.arange(length)[None] * 5 + index) % 31
+        expected_logits, cache = dref.prefill(ids, host_weights)
+        exact_logits, exact_cache = dref.forward(ids, exact)
+        before = pools[1].clone()
+        eager_logits = dec.prefill_paged(ids.to(device), weights, eager, request)
+        got = graph.step(ids.to(device), request)
+        torch.cuda.synchronize()
+        assert got.shape == (1, 1, 31) and got.dtype == torch.float16
+        torch.testing.assert_close(got.cpu(), expected_logits[:, -1:], atol=5e-3, rtol=5e-3)
+        _as_accurate(got, expected_logits[:, -1:], exact_logits[:, -1:])
+        torch.testing.assert_close(got[0, 0], eager_logits[0, -1], atol=5e-3, rtol=5e-3)
+        assert graphed.capacity() == eager.capacity()
+        assert graphed.cached_length(request) == eager.cached_length(request) == length
+        assert graphed.block_table(request) == eager.block_table(request)
+        cached = _pool_cache(graphed, request)
+        for layer in range(22):
+            for kind in range(2):
+                if layer == 0:
+                    torch.testing.assert_close(cached[0][kind], cache[0][kind], atol=2e-3, rtol=2e-3)
+                _as_accurate(cached[layer][kind], cache[layer][kind], exact_cache[layer][kind])
+        written = torch.zeros(pools[1].shape[2:4], dtype=torch.bool, device=device)
+        for position in range(length):
+            block, slot = divmod(position, 16)
+            written[graphed.block_table(request)[block], slot] = True
+        assert torch.equal(pools[1][:, :, ~written].view(torch.int16), before[:, :, ~written].view(torch.int16))
+        torch.randn(1000, device=device).sum().item()  # unrelated eager work between replays
+    counts = graphed.capacity()
+    graphed.create(KVReservation(RequestId("long"), 9))
+    with pytest.raises(ValueError, match="1 to 128 positions"):
+        graph.step(torch.zeros((1, 129), dtype=torch.int64, device=device), RequestId("long"))
+    with pytest.raises(ValueError, match="empty request cache"):
+        graph.step(torch.zeros((1, 4), dtype=torch.int64, device=device), RequestId("q1"))
+    graphed.create(KVReservation(RequestId("small"), 1))
+    with pytest.raises(RuntimeError, match="reservation"):
+        graph.step(torch.zeros((1, 17), dtype=torch.int64, device=device), RequestId("small"))
+    assert graphed.cached_length(RequestId("long")) == graphed.cached_length(RequestId("small")) == 0
+    assert graphed.capacity().owned_blocks == counts.owned_blocks
+
+
 # ---------------------------------------------------------------------------------------
 # Prompt attention (pc_prefill_attention)
 # ---------------------------------------------------------------------------------------
@@ -589,8 +646,8 @@ def _generate_alone(weights, request, device):
         selected.append(int(logits[0, -1].argmax()))
 
 
-@pytest.mark.parametrize("graph_batch", [None, 3, (2, 4)])
-def test_worker_streams_equal_each_request_generated_alone(device, graph_batch):
+@pytest.mark.parametrize("graph_batch, prompt_graphs", [(None, ()), (3, ()), ((2, 4), (16, 48))])
+def test_worker_streams_equal_each_request_generated_alone(device, graph_batch, prompt_graphs):
     """Continuous batching (requests joining and leaving the decode batch every few steps)
     gives every request exactly the tokens it gets when generated by itself."""
     from pagedcore_amd.worker import DecodeWorker, GenerationRequest
@@ -598,7 +655,7 @@ def test_worker_streams_equal_each_request_generated_alone(device, graph_batch):
     weights = _synthetic(device)
     pool = torch.full((22, 2, 48, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
     allocator = KVAllocator(pool)
-    worker = DecodeWorker(weights, allocator, max_active=3, graph_batch=graph_batch)
+    worker = DecodeWorker(weights, allocator, max_active=3, graph_batch=graph_batch, prefill_graph_tokens=prompt_graphs)
     gen = torch.Generator().manual_seed(13)
     requests = []
     for index in range(7):

@@ -192,3 +192,41 @@ def test_decode_steps_replay_the_smallest_graph_that_holds_the_batch(monkeypatch
     for bad in (0, (2, 0), True, (3.0,)):
         with pytest.raises(ValueError, match="graph batch sizes"):
             DecodeWorker(None, allocator, prefill=model.prefill, decode=model.decode, graph_batch=bad)
+
+
+def test_admissions_replay_the_smallest_prefill_graph_that_holds_the_prompt(monkeypatch):
+    """With prefill graph sizes (8, 32) a prompt of T positions replays the PrefillGraph of
+    the smallest size >= T (captured once); a longer prompt runs the prefill function."""
+    from pagedcore_amd import decoder
+
+    model = ScriptedModel()
+    made, used = [], []
+
+    class RecordingPrefillGraph:
+        def __init__(self, weights, allocator, tokens):
+            made.append(tokens)
+            self.tokens, self.allocator = tokens, allocator
+
+        def step(self, ids, rid):
+            assert ids.shape[1] <= self.tokens
+            used.append((self.tokens, ids.shape[1]))
+            return model.prefill(ids, None, self.allocator, rid)[:, -1:]
+
+    monkeypatch.setattr(decoder, "PrefillGraph", RecordingPrefillGraph)
+    allocator = cpu_allocator(torch.zeros((22, 2, 32, 16, 4, 64), dtype=torch.float16))
+    worker = DecodeWorker(None, allocator, max_active=4, prefill=model.prefill, decode=model.decode,
+                          prefill_graph_tokens=[32, 8])
+    requests = [_request("a", prompt=8), _request("b", prompt=9), _request("c", prompt=40), _request("d", prompt=3)]
+    _submit(worker, model, requests)
+    results = worker.run()
+    assert used == [(8, 8), (32, 9), (8, 3)]
+    assert model.prefills == ["a", "b", "c", "d"]  # c (40 positions) ran the prefill function
+    assert made == [8, 32]
+    assert all(results[r.request_id].greedy_ids == (10, 11, 12, 13) for r in requests)
+    captured = []
+    monkeypatch.setattr(decoder, "PrefillGraph", lambda weights, allocator, tokens: captured.append(tokens))
+    DecodeWorker(None, allocator, prefill=model.prefill, decode=model.decode, prefill_graph_tokens=(64, 2048)).capture_graphs()
+    assert captured == [64, 2048]
+    for bad in ((0,), (2049,), (True,), (16.0,)):
+        with pytest.raises(ValueError, match="prefill graph sizes"):
+            DecodeWorker(None, allocator, prefill=model.prefill, decode=model.decode, prefill_graph_tokens=bad)
