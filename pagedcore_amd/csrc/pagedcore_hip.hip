@@ -344,11 +344,18 @@ __global__ __launch_bounds__(kItemThreads) __attribute__((amdgpu_waves_per_eu(6,
   const int c = lane & 15;
   const int g = lane >> 4;
 
-  // The whole plan record in one scalar load; this wave's block ids are selected from it.
+  // The whole plan record in one round trip; this wave's block ids are selected from it.
+  // The empty asm makes every word (and every kernel argument the loads below need) an
+  // input before the first branch: otherwise those loads sink below the early exits, and
+  // each becomes one more dependent round trip, queued behind the K/V loads of the
+  // workgroups already running (microseconds each).
   const int32_t* rec = a.plan + static_cast<int64_t>(blockIdx.x) * kPlanInts;
   int32_t r[kPlanInts];
 #pragma unroll
   for (int i = 0; i < kPlanInts; ++i) r[i] = rec[i];
+  asm volatile("" ::"s"(r[0]), "s"(r[1]), "s"(r[2]), "s"(r[4]), "s"(r[5]), "s"(r[6]), "s"(r[7]), "s"(r[8]), "s"(r[9]),
+               "s"(r[10]), "s"(r[11]), "s"(r[12]), "s"(a.batch), "s"(a.max_blocks), "s"(a.max_items), "s"(a.pool),
+               "s"(a.query), "s"(a.num_blocks), "s"(a.layer));
   const int b = r[0];
   const int item = r[1];
   const int len = r[2];
