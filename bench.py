@@ -29,6 +29,8 @@ import time
 
 import numpy as np
 import torch
+from typing import Sequence
+from torch import Tensor
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
@@ -171,7 +173,53 @@ def _captured(fn, device: torch.device) -> torch.cuda.CUDAGraph:
     return graph
 
 
-def run_long_context(steps: int, warmup: int) -> dict:
+def cpu_long_context_baseline(pool: Tensor, queries: Tensor, new_kv: Tensor, w: workloads.BatchedDecode,
+                              seconds: float) -> dict:
+    """The oracle's ports of the reference's per-row decode work on the CPU, per sequence of
+    one layer: write_decode_layer's copies of the new token (kv_cache.py:242-245) and one
+    paged_attention call over its 2048 tokens (attention.py:14-53, as decoder.py:182-190
+    calls it), on all host threads. Sequences are taken in order (cycling the 22 layers)
+    for about `seconds`; the per-step figure scales the mean per-sequence time to the
+    batch x 22 layers. Copying the sampled blocks to host memory is not timed."""
+    from oracle import paged_reference as ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    done, elapsed, row = 0, 0.0, 0
+    while elapsed < seconds:
+        layer, b = divmod(row, w.batch)
+        layer %= LAYERS
+        length = int(w.lengths[b])
+        table = [int(x) for x in w.tables[b, : (length + 15) // 16]]
+        index = torch.tensor(table, dtype=torch.long, device=pool.device)
+        sub = torch.empty((LAYERS, 2, len(table), 16, 4, 64), dtype=torch.float16)
+        sub[layer] = pool[layer].index_select(1, index).cpu()
+        host = sub.view(torch.int16).numpy().view(np.uint16)
+        key = new_kv[0, layer, b].cpu().view(torch.int16).numpy().view(np.uint16)
+        value = new_kv[1, layer, b].cpu().view(torch.int16).numpy().view(np.uint16)
+        query = queries[layer, b].reshape(1, 32, 1, 64).cpu()
+        local = list(range(len(table)))
+        start = time.perf_counter()
+        ref.reference_write_decode(host, layer, local, length, key, value)
+        ref.reference_paged_attention(query, sub, layer, local, length)
+        elapsed += time.perf_counter() - start
+        done += 1
+        row += 1
+    per_row = elapsed / done
+    step_s = per_row * w.batch * LAYERS
+    per_step_bytes = (attention_bytes(w.lengths) + w.batch * 1024 * 2) * LAYERS
+    return {
+        "value": round(per_step_bytes / step_s / 1e9, 4),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{done} sequence-layers of the same workload (append of the new token + one reference paged_attention "
+        f"call over 2048 tokens each), {elapsed:.1f} s on {cores} threads, {per_row * 1e3:.2f} ms per sequence-layer; "
+        f"scaled to {w.batch} sequences x 22 layers: {step_s:.2f} s per step, {w.batch / step_s:.2f} decode tokens/s",
+    }
+
+
+def run_long_context(steps: int, warmup: int, cpu_seconds: float = 0.0) -> dict:
     """Long-context, high-occupancy decode: batch 256, every sequence at 2047 cached tokens
     (128 blocks), a fully shuffled 40000-block pool, 22 layers. Per layer the step appends
     each sequence's new token (pc_kv_append, slot 2047) and then runs attention over 2048
@@ -218,7 +266,7 @@ def run_long_context(steps: int, warmup: int) -> dict:
     attn = attention_bytes(w.lengths)
     append = w.batch * 1024 * 2  # read the new K/V rows, write them to their slots
     per_step = (attn + append) * LAYERS
-    return {
+    result = {
         "workload": "batch 256, every sequence 2047 cached + 1 appended (128 blocks), 40000-block shuffled pool, "
         "22 layers; per layer pc_kv_append of the 256 new tokens + pc_paged_decode_attn, replayed as one graph",
         "ms_per_step": round(total_ms / steps, 4),
@@ -228,9 +276,42 @@ def run_long_context(steps: int, warmup: int) -> dict:
         "bytes_per_layer": attn + append,
         "us_per_layer": round(total_ms / steps / LAYERS * 1e3, 3),
     }
+    if cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_long_context_baseline(pool, queries, new_kv, w, cpu_seconds)
+    return result
 
 
-def run_prompt_append(steps: int) -> dict:
+def cpu_append_baseline(w: workloads.PromptAppend, table: Sequence[int], seconds: float) -> dict:
+    """The oracle's port of KVAllocator.append's chunked copies (kv_cache.py:161-172): the
+    same 2048-token prompt (K and V of 22 layers) in the same 128 chunk copies per kind, one
+    thread (numpy slice copies, as the reference's CPU tensor copies), repeated for about
+    `seconds` after one untimed append that faults the pages in. The host pool holds just
+    the prompt's 128 blocks, in table order (a 1.4 GB host pool would only add page
+    faults). The allocator's Python bookkeeping is not included."""
+    from oracle import paged_reference as ref
+
+    key, value = (a.view(np.uint16) for a in w.prompt_kv())
+    pool = np.zeros((LAYERS, 2, len(table), 16, 4, 64), dtype=np.uint16)
+    compact = list(range(len(table)))
+    ref.reference_append(pool, compact, 0, key, value)
+    done, elapsed = 0, 0.0
+    while elapsed < seconds:
+        start = time.perf_counter()
+        ref.reference_append(pool, compact, 0, key, value)
+        elapsed += time.perf_counter() - start
+        done += 1
+    nbytes = 2 * 2 * LAYERS * w.prompt_tokens * 256 * 2
+    return {
+        "value": round(nbytes * done / elapsed / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{done} whole appends of the same 2048-token prompt (128 blocks), {elapsed:.1f} s on one thread; "
+        f"{elapsed / done * 1e3:.2f} ms per append",
+    }
+
+
+def run_prompt_append(steps: int, cpu_seconds: float = 0.0) -> dict:
     """Prompt KV append: one 2048-token prompt's K and V (22 layers, N(0, 1) fp16) into a
     4096-block pool whose free list is in seeded random order with 30% of it held by 10
     filler requests, so the prompt's 128 blocks are scattered. The allocator's append is
@@ -269,7 +350,7 @@ def run_prompt_append(steps: int) -> dict:
     total_ms = _timed(graph.replay, 1, device)
     nbytes = 2 * 2 * LAYERS * w.prompt_tokens * 256 * 2  # K and V, read once and written once
     us = total_ms / steps * 1e3
-    return {
+    result = {
         "workload": "2048-token prompt x 22 layers (K and V [22,2048,4,64] fp16) into a 4096-block pool, 30% held by "
         f"10 filler requests, free list in seeded random order ({scattered} discontinuities in the 128-block table)",
         "us_per_append": round(us, 3),
@@ -278,6 +359,9 @@ def run_prompt_append(steps: int) -> dict:
         "bytes_per_append": nbytes,
         "allocator_append_ms": round(api_ms, 3),
     }
+    if cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_append_baseline(w, [int(b) for b in table], cpu_seconds)
+    return result
 
 
 def run_prefill(steps: int) -> dict:
@@ -500,6 +584,7 @@ def cpu_baseline(layers: DecodeLayers, seconds: float) -> dict:
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_decode_attention_b64_hbm_traffic.txt")
+EXTRA_CPU_SECONDS = 3.0  # CPU baseline sample of each extra workload that has one
 
 
 def measured_traffic() -> int | None:
@@ -533,15 +618,16 @@ def calibration_copy(mib: int, device: torch.device) -> None:
     del src, dst
 
 
-def run_extra(selected: set, steps: int) -> dict:
-    """The workloads beside the headline, each reported as its own object."""
+def run_extra(selected: set, steps: int, cpu_seconds: float = 0.0) -> dict:
+    """The workloads beside the headline, each reported as its own object (with a CPU
+    baseline of about `cpu_seconds` where the workload has one; 0 = none)."""
     extra = {}
     if "prompt_append" in selected:
-        extra["prompt_append"] = run_prompt_append(max(10, steps))
+        extra["prompt_append"] = run_prompt_append(max(10, steps), cpu_seconds)
         torch.cuda.empty_cache()
         print(f"prompt append: {extra['prompt_append']}", file=sys.stderr, flush=True)
     if "long_context" in selected:
-        extra["long_context_b256"] = run_long_context(max(5, steps // 5), 2)
+        extra["long_context_b256"] = run_long_context(max(5, steps // 5), 2, cpu_seconds)
         torch.cuda.empty_cache()
         print(f"long context: {extra['long_context_b256']}", file=sys.stderr, flush=True)
     if "prefill" in selected:
@@ -594,7 +680,7 @@ def main() -> int:
     if "attention" not in selected:
         # Diagnostic run of the other workloads alone (e.g. to profile one of them); the
         # headline line needs the attention workload.
-        extra = run_extra(selected, args.steps)
+        extra = run_extra(selected, args.steps, 0.0 if args.no_cpu_baseline else EXTRA_CPU_SECONDS)
         print(json.dumps({"diagnostic": True, **extra}), flush=True)
         return 0
     r = run_decode(args.steps, args.warmup, use_graph=not args.no_graph)
@@ -612,7 +698,7 @@ def main() -> int:
         baseline = cpu_baseline(layers, args.cpu_seconds)
     del layers, r["layers"]
     torch.cuda.empty_cache()
-    extra = run_extra(selected, args.steps)
+    extra = run_extra(selected, args.steps, 0.0 if args.no_cpu_baseline else EXTRA_CPU_SECONDS)
 
     record = {
         "metric": "paged-decode attn HBM GB/s (% of ~8 TB/s peak) + decode tok/s, batch 64 ctx<=2048",
