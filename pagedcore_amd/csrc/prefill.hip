@@ -5,22 +5,27 @@
 // pc_rope_kv_append wrote), o [T][32][64], all fp16.
 //
 // Work split: one workgroup per (16-query block, kv head), longest (latest) blocks first; its
-// 8 waves are the 8 query heads of the kv head, so each K/V block is fetched once per
-// workgroup (the waves share it through L1). A wave walks key blocks 0 .. its query block
-// with an online softmax in fp32:
+// 8 waves are the 8 query heads of the kv head. Each 16-key block of K and V is staged in
+// LDS once per workgroup (LDS DMA by four of the waves, two buffers, one barrier per block)
+// and read by all eight waves. A wave walks key blocks 0 .. its query block with an online
+// softmax in fp32:
 //   S^T = K_blk . Q^T   on v_mfma_f32_16x16x32_f16 (lane (c, g): keys 4g..4g+3 of position c)
-//   O^T += V^T . P^T    on v_mfma_f32_16x16x16f16, V^T from the transposing LDS reads of the
-//                       decode kernel's V layout, P^T straight from the S^T registers
+//   O^T += V^T . P^T    on v_mfma_f32_16x16x16f16, V^T from the decode kernel's transposing
+//                       LDS reads, P^T straight from the S^T registers
+//   l   += 1 . P^T      one more v_mfma_f32_16x16x16f16 with an all-ones A operand: the
+//                       softmax denominator of every position, summed on the matrix core
 // so every per-position quantity (running max, sum, rescale) stays in the lane that owns
-// the position. K and V of the next block move to LDS by DMA while the current block is
-// processed (two buffers per wave). Probabilities enter the PV
-// product as fp16 (relative error 2^-11) and the normalising sum adds those same fp16
-// weights; everything else is fp32 with one final fp16 rounding.
+// the position. Only the diagonal block needs the causal mask. Probabilities enter the PV
+// product as fp16 (relative error 2^-11) and the denominator sums those same fp16 weights;
+// everything else is fp32 with one final fp16 rounding.
 
 #include <hip/hip_runtime.h>
 
 #include <math.h>
 #include <stdint.h>
+
+#include <type_traits>
+#include <utility>
 
 #include "pagedcore_hip.h"
 #include "pc_device.h"
@@ -41,9 +46,27 @@ constexpr int kWaves = kQHeads / kKVHeads;  // 8 query heads per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBlock = 16;                   // positions per query block and keys per key block
 constexpr int kTileBytes = kBlock * kHeadDim * 2;  // 16 rows of one kv head: 2 KiB
-constexpr int kBufBytes = 2 * kTileBytes;           // K tile, then V tile
+constexpr int kBufBytes = 2 * kTileBytes;           // one key block: K tile, then V tile
+constexpr int kStepBlocks = 4;                      // key blocks per step (a multiple of 2)
+constexpr int kStageBytes = kStepBlocks * kBufBytes;
 constexpr int kMaxTokens = 1 << 16;
 constexpr float kLazyLog2 = 8.0f;            // headroom (log2 of p) before the running max is raised
+
+// f(integral_constant<int, p>) for every pair p of key blocks of a step, in order.
+template <typename F, int... P>
+__device__ __forceinline__ void for_pairs_impl(F&& f, std::integer_sequence<int, P...>) {
+  (f(std::integral_constant<int, P>{}), ...);
+}
+template <typename F>
+__device__ __forceinline__ void for_pairs(F&& f) {
+  for_pairs_impl(f, std::make_integer_sequence<int, kStepBlocks / 2>{});
+}
+
+// Two 16-key tiles as one 32-key MFMA operand (first tile's keys first).
+__device__ __forceinline__ half8_t join(short4_t x, short4_t y) {
+  const half4_t a = __builtin_bit_cast(half4_t, x), b = __builtin_bit_cast(half4_t, y);
+  return half8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
 
 struct PrefillArgs {
   _Float16* out;
@@ -54,7 +77,9 @@ struct PrefillArgs {
 };
 
 __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) char lds[kWaves][2][kBufBytes];
+  // Two stages of kStepBlocks key blocks each: stage s, block b: K tile at s * kStageBytes +
+  // b * kBufBytes, its V tile kTileBytes after it.
+  __shared__ __attribute__((aligned(16))) char lds[2][kStageBytes];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int c = lane & 15;
@@ -66,108 +91,139 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillArgs
   const int pos = kBlock * qb + c;  // this lane's query position (column of S^T)
   const int last = a.tokens - 1;
 
-  // Q is loaded once with ordinary loads. K and V of each key block arrive by LDS DMA into
-  // one of two buffers (waited for explicitly), so no register is ever the target of a load
-  // still in flight across loop iterations.
   const _Float16* qrow = a.q + (static_cast<int64_t>(min(pos, last)) * kQHeads + head) * kHeadDim + 8 * g;
-  const half8_t qa = *reinterpret_cast<const half8_t*>(qrow);
-  const half8_t qc = *reinterpret_cast<const half8_t*>(qrow + 32);
+  half8_t qa = *reinterpret_cast<const half8_t*>(qrow);
+  half8_t qc = *reinterpret_cast<const half8_t*>(qrow + 32);
 
-  // DMA lane mapping (64 lanes x 16 B = 8 rows of 128 B per instruction): lane moves piece
-  // qs of rows r8 and r8 + 8. K piece p of row r sits at position p ^ (r & 7) (the A-operand
-  // reads of 16 rows then hit 8 different 16 B bank groups); V uses the decode kernel's
-  // 32 B-group swizzle for its transposing reads.
-  const int qs = lane & 7, r8 = lane >> 3;
-  const int kpieceA = qs ^ (r8 & 7), kpieceB = qs ^ ((r8 + 8) & 7);
-  const int vpieceA = 2 * ((qs >> 1) ^ row_sel(r8)) + (qs & 1);
-  const int vpieceB = 2 * ((qs >> 1) ^ row_sel(r8 + 8)) + (qs & 1);
-  const uint32_t buf0 = lds_offset(lds[w][0]);
+  // Staging: every wave issues kStepBlocks / 2 LDS DMA instructions per stage (each 64 lanes
+  // x 16 B = rows srow .. srow + 7 of one tile): wave w stages blocks w / 4, w / 4 + 2, ...
+  // of the step, the K (w & 2 = 0) or V tile, rows 8 (w & 1) .. 8 (w & 1) + 7. K piece p of
+  // row r sits at position p ^ (r & 7) (the A-operand reads of 16 rows then hit 8 different
+  // 16 B bank groups); V uses the decode kernel's 32 B-group swizzle for its transposing
+  // reads.
+  const bool stage_v = (w & 2) != 0;
+  const int sblock = w >> 2;
+  const int qs = lane & 7;
+  const int srow = 8 * (w & 1) + (lane >> 3);
+  const int piece = stage_v ? 2 * ((qs >> 1) ^ row_sel(srow)) + (qs & 1) : qs ^ (srow & 7);
+  const _Float16* ssrc = (stage_v ? a.v : a.k) + h * kHeadDim + 8 * piece;
+  const int sdst = sblock * kBufBytes + (stage_v ? kTileBytes : 0) + 1024 * (w & 1);
+  const uint32_t lds0 = lds_offset(lds[0]);
   // K reads: lane (c, g) takes row c, pieces g and 4 + g
-  const uint32_t kaddr0 = buf0 + c * 128 + 16 * (g ^ (c & 7));
-  const uint32_t kaddr1 = buf0 + c * 128 + 16 * ((4 + g) ^ (c & 7));
+  const uint32_t kaddr0 = lds0 + c * 128 + 16 * (g ^ (c & 7));
+  const uint32_t kaddr1 = lds0 + c * 128 + 16 * ((4 + g) ^ (c & 7));
   // V transposing reads: lane (c, g) supplies row 4g + c/4, 8 B piece c % 4
   const int rr = 4 * g + (c >> 2);
-  const uint32_t vbase = buf0 + kTileBytes + rr * 128 + 8 * (c & 3);
+  const uint32_t vbase = lds0 + kTileBytes + rr * 128 + 8 * (c & 3);
   const uint32_t tsel = row_sel(rr);
 
-  auto issue = [&](int kb, int buf) {
-    char* dst = lds[w][buf];
-    const int ra = min(kBlock * kb + r8, last), rb = min(kBlock * kb + r8 + 8, last);
-    const _Float16* ka = a.k + (static_cast<int64_t>(ra) * kKVHeads + h) * kHeadDim;
-    const _Float16* kb8 = a.k + (static_cast<int64_t>(rb) * kKVHeads + h) * kHeadDim;
-    const _Float16* va = a.v + (static_cast<int64_t>(ra) * kKVHeads + h) * kHeadDim;
-    const _Float16* vb8 = a.v + (static_cast<int64_t>(rb) * kKVHeads + h) * kHeadDim;
-    __builtin_amdgcn_global_load_lds(static_cast<const void*>(ka + 8 * kpieceA), lds_ptr(dst), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(static_cast<const void*>(kb8 + 8 * kpieceB), lds_ptr(dst + 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(static_cast<const void*>(va + 8 * vpieceA), lds_ptr(dst + kTileBytes), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb8 + 8 * vpieceB), lds_ptr(dst + kTileBytes + 1024), 16,
-                                     0, 0);
-    __builtin_amdgcn_sched_barrier(0);  // keep the issue order the waits count on
+  // Key blocks kStepBlocks * j .. + kStepBlocks - 1 into stage `buf` (rows past the prompt
+  // repeat its last row; their scores are masked).
+  auto stage = [&](int j, int buf) {
+#pragma unroll
+    for (int i = 0; i < kStepBlocks / 2; ++i) {
+      const int row = min(kBlock * (kStepBlocks * j + sblock + 2 * i) + srow, last);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(ssrc + static_cast<int64_t>(row) * kKVHeads * kHeadDim),
+                                       lds_ptr(lds[buf] + sdst + 2 * i * kBufBytes), 16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   };
 
-  float m = 0.f, mc = 0.f, lsum = 0.f;
-  float4_t acc[4];
+  const half8_t ones = {1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
+  float m = 0.f, mc = 0.f;
+  float4_t acc[4], lacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int u = 0; u < 4; ++u) acc[u] = float4_t{0.f, 0.f, 0.f, 0.f};
-  const int nkb = qb + 1;  // causal: key blocks 0 .. qb
+  const int steps = (qb + kStepBlocks) / kStepBlocks;  // causal: key blocks 0 .. qb
 
-  issue(0, 0);
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    const bool more = kb + 1 < nkb;
-    // The other buffer was last read in the previous iteration (its reads waited for
-    // lgkmcnt(0)), so it can be refilled; then this block's four DMAs are complete once at
-    // most the next block's four are pending.
-    if (more) {
-      issue(kb + 1, buf ^ 1);
-      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    half8_t k0, k1;
-    asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
-                 : "=&v"(k0), "=&v"(k1)
-                 : "v"(kaddr0 + buf * kBufBytes), "v"(kaddr1 + buf * kBufBytes)
-                 : "memory");
-    float4_t sv = {0.f, 0.f, 0.f, 0.f};
-    sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qa, sv, 0, 0, 0);
-    sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qc, sv, 0, 0, 0);
-    float sc[4];
+  // One step over the key blocks of step j, staged in stage B (a compile-time constant, so
+  // every LDS address below is a fixed base plus an immediate offset).
+  auto step = [&](int j, auto stage_index) {
+    constexpr int B = decltype(stage_index)::value;
+    constexpr uint32_t so = B * kStageBytes;
+    // This wave's staging of step j (and, before the first step, Q) has landed; after the
+    // barrier every wave's has, and every wave has finished reading the other stage (its
+    // reads of step j - 1 waited for lgkmcnt(0)), which the next staging refills. Q is named
+    // so that the compiler does not add a wait of its own for it, which would also wait for
+    // the staging issued below.
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(qa), "+v"(qc) : : "memory");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < steps) stage(j + 1, B ^ 1);
+    // sc[4 b + e]: key 4g + e of block kStepBlocks * j + b
+    float sc[4 * kStepBlocks];
+    auto scores = [&](auto pair) {
+      constexpr int b = 2 * decltype(pair)::value;
+      half8_t k00, k01, k10, k11;
+      asm volatile(
+          "ds_read_b128 %0, %4 offset:%6\n\tds_read_b128 %1, %5 offset:%6\n\tds_read_b128 %2, %4 offset:%7\n\t"
+          "ds_read_b128 %3, %5 offset:%7\n\ts_waitcnt lgkmcnt(0)"
+          : "=&v"(k00), "=&v"(k01), "=&v"(k10), "=&v"(k11)
+          : "v"(kaddr0), "v"(kaddr1), "i"(so + b * kBufBytes), "i"(so + (b + 1) * kBufBytes)
+          : "memory");
+      float4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k00, qa, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k10, qa, s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k01, qc, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k11, qc, s1, 0, 0, 0);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int key = kBlock * kb + 4 * g + e;
-      sc[e] = (key <= pos && key <= last) ? sv[e] : -INFINITY;
+      for (int e = 0; e < 4; ++e) {
+        sc[4 * b + e] = s0[e];
+        sc[4 * b + 4 + e] = s1[e];
+      }
+    };
+    for_pairs(scores);
+    if (kStepBlocks * j + kStepBlocks - 1 >= qb) {  // the diagonal step: keys after the position, or past the prompt, are masked
+#pragma unroll
+      for (int e = 0; e < 4 * kStepBlocks; ++e) {
+        const int key = kBlock * (kStepBlocks * j + (e >> 2)) + 4 * g + (e & 3);
+        sc[e] = (key <= pos && key <= last) ? sc[e] : -INFINITY;
+      }
     }
-    const float bm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    if (kb == 0) {
+    float bm = sc[0];
+#pragma unroll
+    for (int e = 1; e < 4 * kStepBlocks; ++e) bm = fmaxf(bm, sc[e]);
+    if (j == 0) {
       m = max_over_groups(bm);  // finite: key 0 is visible to every position
       mc = m * kScoreToLog2;
     } else if (__builtin_amdgcn_ballot_w64(bm * kScoreToLog2 > mc + kLazyLog2) != 0) {
       const float mn = fmaxf(m, max_over_groups(bm));
       const float alpha = exp2_fast((m - mn) * kScoreToLog2);
-      lsum *= alpha;
+      lacc *= alpha;
 #pragma unroll
       for (int u = 0; u < 4; ++u) acc[u] *= alpha;
       m = mn;
       mc = m * kScoreToLog2;
     }
-    half4_t pb;
+    // Per pair of blocks, P^T as one 32-key B operand: element e is key 4g + (e & 3) of
+    // the pair's block e / 4; the V^T A operands concatenate the two blocks in the same
+    // order.
+    auto accumulate = [&](auto pair) {
+      constexpr int b = 2 * decltype(pair)::value;
+      half8_t pb;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      // the sum takes the fp16 weights the PV product uses, so constant V comes back exactly
-      pb[e] = static_cast<_Float16>(exp2_fast(fmaf(sc[e], kScoreToLog2, -mc)));
-      lsum += static_cast<float>(pb[e]);
-    }
-    short4_t v0, v1, v2, v3;
-    read_v_tiles<0>(vbase + buf * kBufBytes, tsel, v0, v1, v2, v3);
-    acc[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, v0), pb, acc[0], 0, 0, 0);
-    acc[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, v1), pb, acc[1], 0, 0, 0);
-    acc[2] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, v2), pb, acc[2], 0, 0, 0);
-    acc[3] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, v3), pb, acc[3], 0, 0, 0);
+      for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(exp2_fast(fmaf(sc[4 * b + e], kScoreToLog2, -mc)));
+      short4_t a0, a1, a2, a3, b0, b1, b2, b3;
+      read_v_tiles<so + b * kBufBytes>(vbase, tsel, a0, a1, a2, a3);
+      read_v_tiles<so + (b + 1) * kBufBytes>(vbase, tsel, b0, b1, b2, b3);
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(join(a0, b0), pb, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(join(a1, b1), pb, acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(join(a2, b2), pb, acc[2], 0, 0, 0);
+      acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(join(a3, b3), pb, acc[3], 0, 0, 0);
+      lacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb, lacc, 0, 0, 0);
+    };
+    for_pairs(accumulate);
+  };
+
+  stage(0, 0);
+  for (int j = 0; j < steps; j += 2) {
+    step(j, std::integral_constant<int, 0>{});
+    if (j + 1 < steps) step(j + 1, std::integral_constant<int, 1>{});
   }
 
-  // lane (c, g) of tile u holds O^T[dims 16u + 4g .. + 3][position c]
-  const float inv = 1.0f / sum_over_groups(lsum);
+  // lane (c, g) of tile u holds O^T[dims 16u + 4g .. + 3][position c]; every row of lacc
+  // holds the denominator of position c
+  const float inv = 1.0f / lacc[0];
   if (pos <= last) {
     _Float16* dst = a.out + (static_cast<int64_t>(pos) * kQHeads + head) * kHeadDim + 4 * g;
 #pragma unroll

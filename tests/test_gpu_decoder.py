@@ -536,7 +536,7 @@ def _causal_fp64(query, key, value):
     return (scores.softmax(-1) @ v).transpose(0, 1)
 
 
-@pytest.mark.parametrize("tokens", [1, 15, 16, 17, 100, 333, 2048])
+@pytest.mark.parametrize("tokens", [1, 15, 16, 17, 64, 65, 100, 333, 1000, 2048])
 def test_prefill_attention_matches_fp32_and_fp64(device, tokens):
     """Against the reference's fp32 dense attention (dense.py:91-99, causal) and FP64, both
     within 2e-3; positions past the prompt are never written."""
