@@ -653,11 +653,11 @@ def main() -> int:
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-graph", action="store_true", help="launch from Python instead of replaying a HIP graph")
-    parser.add_argument("--workloads", default="attention,prompt_append,long_context,prefill,decode_step",
+    parser.add_argument("--workloads", default="attention,prompt_append,long_context,prefill,decode_step,serving",
                         help="comma list: attention (the headline; without it only the others run, as a diagnostic line), prompt_append (2048-token prompt into a "
                         "fragmented pool), long_context (batch 256 x 2048, append + attention), prefill (one 2048-token "
                         "prompt through the model), decode_step (full TinyLlama-architecture step, batch 128), serving "
-                        "(continuous batching of 128 requests; not in the default run)")
+                        "(continuous batching of 128 requests)")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="run one plain copy of this many MiB first (counter calibration under rocprofv3 --pmc)")
     args = parser.parse_args()
