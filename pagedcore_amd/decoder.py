@@ -294,7 +294,7 @@ MAX_BLOCKS = CONTEXT_LIMIT // 16  # 128: the widest block table of a request
 
 
 class DecodeGraph:
-    """decode_paged for a fixed batch size, captured once as a HIP graph and replayed.
+    """decode_paged for batches of up to a fixed size, captured once as a HIP graph and replayed.
 
     A decode step is about 200 launches (9 per layer); issued one by one from Python they
     cost more host time than the GPU needs to run them. Here the step's device work is

@@ -269,6 +269,36 @@ def test_batched_decode_b64_matches_oracle(device, order):
         torch.testing.assert_close(got, fp64, **TOL, msg=lambda m: f"row {b} len {w.lengths[b]} fp64: {m}")
 
 
+def test_work_item_boundaries_match_oracle(device):
+    """Lengths on both sides of the 9-block (144-token) work-item boundaries -- one item
+    exactly filled, a one-token second item, 8, 9 and 15 items, a single token and a single
+    block -- in one ragged batch over a shuffled pool: every row against the oracle and
+    FP64."""
+    lengths = np.array([143, 144, 145, 287, 288, 289, 1151, 1152, 1153, 1295, 1296, 1297, 2047, 2048, 1, 16],
+                       dtype=np.int32)
+    _say("item boundaries", lengths.tolist())
+    need = (lengths + 15) // 16
+    num_blocks = 1024
+    perm = np.random.default_rng(77).permutation(num_blocks).astype(np.int32)
+    tables = np.zeros((len(lengths), int(need.max())), dtype=np.int32)
+    offset = 0
+    for b, n in enumerate(need):
+        tables[b, :n] = perm[offset : offset + n]
+        offset += int(n)
+    w = workloads.BatchedDecode(lengths, tables, num_blocks, 77)
+    pool = _random_pool(device, num_blocks, 13)
+    layer = 9
+    queries = torch.from_numpy(w.queries(layer)).to(device)
+    out = torch.full_like(queries, float("nan"))
+    _hip.paged_decode_attention(out, queries, pool, layer, torch.from_numpy(tables).to(device),
+                                torch.from_numpy(lengths).to(device))
+    torch.cuda.synchronize()
+    for b, (oracle, fp64) in _oracle_rows(pool, layer, w, queries, range(len(lengths))).items():
+        got = out[b : b + 1].reshape(1, 32, 1, 64).cpu()
+        torch.testing.assert_close(got, oracle, **TOL, msg=lambda m: f"row {b} len {lengths[b]}: {m}")
+        torch.testing.assert_close(got, fp64, **TOL, msg=lambda m: f"row {b} len {lengths[b]} fp64: {m}")
+
+
 def test_long_context_b256_full_length(device):
     """Batch 256 at 2048 tokens (128 blocks each, 15 work items) over a fully shuffled
     40000-block pool -- several rounds of workgroups: rows against the oracle, and a
