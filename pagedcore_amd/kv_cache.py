@@ -156,12 +156,15 @@ class StagedDecode:
 @dataclass(slots=True)
 class _DecodeBatch:
     """Device block tables and lengths of one batch of requests, plus their host copies
-    and the decode plan built from them (on first use)."""
+    and the decode plan built from them (on first use). `appends` are the staged appends
+    of the batch's requests when it was built: a later lookup of the same allocator state
+    only has to check that their layer is written."""
 
     tables: Tensor
     lengths: Tensor
     host_tables: np.ndarray
     host_lengths: np.ndarray
+    appends: Tuple["_TokenAppend", ...] = ()
     plan: Optional[Tensor] = None
 
 
@@ -246,6 +249,7 @@ class KVAllocator:
         self._writer = kv_writer
         self._worker = current_thread()
         self._stream = torch.cuda.current_stream(pool.device) if pool.is_cuda else None
+        self._stream_handle = self._stream.cuda_stream if self._stream is not None else None
         self._free_blocks = _CountingList(BlockId(index) for index in reversed(range(pool.shape[2])))
         self._sequences: Dict[RequestId, _SequenceCache] = _CountingDict()
         # Tables are checked against the owners recorded when blocks are assigned.
@@ -707,10 +711,15 @@ class KVAllocator:
         self._check_staged_state(request_ids)
         if type(layer_index) is not int or not 0 <= layer_index < LAYERS:
             raise ValueError("layer_index must identify one of the 22 decoder layers")
-        sequences = [self._staged_sequence(request_id, layer_index) for request_id in request_ids]
         staged = self._decode_appends is not None
         key = (self._version, tuple(request_ids), staged)
         cached = self._table_cache.get(key)
+        # Same allocator state and requests: the requests exist and are nonempty, so only
+        # the written-layer check of the staged ones can fail; if it would, the full
+        # per-request checks below raise in the reference's order.
+        if cached is not None and all(layer_index < append.written_layers for append in cached.appends):
+            return cached
+        sequences = [self._staged_sequence(request_id, layer_index) for request_id in request_ids]
         if cached is not None:
             return cached
         width = max(len(sequence.blocks) for sequence in sequences)
@@ -719,11 +728,13 @@ class KVAllocator:
         for row, sequence in enumerate(sequences):
             tables[row, : len(sequence.blocks)] = sequence.blocks
             lengths[row] = sequence.length
+        appends = self._decode_appends or {}
         result = _DecodeBatch(
             torch.from_numpy(tables).to(self._pool.device),
             torch.from_numpy(lengths).to(self._pool.device),
             tables,
             lengths,
+            tuple(appends[request_id] for request_id in request_ids if request_id in appends),
         )
         if len(self._table_cache) > 64:
             self._table_cache.clear()
@@ -785,7 +796,7 @@ class KVAllocator:
     def _check_worker(self) -> None:
         if current_thread() is not self._worker:
             raise RuntimeError("KV allocator must be used by its owning model worker")
-        if self._stream is not None and torch.cuda.current_stream(self._pool.device) != self._stream:
+        if self._stream is not None and _hip.current_stream_handle(self._pool.device) != self._stream_handle:
             raise RuntimeError("KV allocator must use its owning CUDA stream")
 
     def _state_key(self) -> Optional[tuple]:
