@@ -299,6 +299,40 @@ def test_work_item_boundaries_match_oracle(device):
         torch.testing.assert_close(got, fp64, **TOL, msg=lambda m: f"row {b} len {lengths[b]} fp64: {m}")
 
 
+@pytest.mark.parametrize("seed", [101, 202, 303, 404])
+def test_random_batches_through_the_allocator_match_fp64(device, seed):
+    """Random batch sizes (1-200) and lengths (1-2048) appended through the allocator into
+    one NaN-poisoned pool, attended with paged_attention_batch at a random layer: every row
+    within 2e-3 of FP64 over the request's gathered history."""
+    rng = np.random.default_rng(seed)
+    batch = int(rng.integers(1, 201))
+    lengths = rng.integers(1, 2049, size=batch)
+    blocks = int(((lengths + 15) // 16).sum()) + 8
+    _say("random batch", seed, batch, int(lengths.sum()))
+    gen = torch.Generator(device=device).manual_seed(seed)
+    pool = torch.full((22, 2, blocks, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    requests = tuple(RequestId(f"s{seed}-{b}") for b in range(batch))
+    for request, length in zip(requests, lengths):
+        allocator.create(KVReservation(request, int((length + 15) // 16)))
+        key = torch.randn(22, int(length), 4, 64, dtype=torch.float16, device=device, generator=gen)
+        value = torch.randn(22, int(length), 4, 64, dtype=torch.float16, device=device, generator=gen)
+        allocator.append(request, key, value)
+    layer = int(rng.integers(0, 22))
+    query = torch.randn(batch, 32, 1, 64, dtype=torch.float16, device=device, generator=gen)
+    out = paged_attention_batch(query, allocator, requests, layer_index=layer)
+    torch.cuda.synchronize()
+    for b, request in enumerate(requests):
+        table = list(allocator.block_table(request))
+        index = torch.tensor(table, dtype=torch.long, device=device)
+        sub = torch.zeros((22, 2, len(table), 16, 4, 64), dtype=torch.float16)
+        sub[layer] = pool[layer].index_select(1, index).cpu()
+        history = ref.gather_history(sub, layer, list(range(len(table))), int(lengths[b]))
+        fp64 = ref.dense_attention_fp64(query[b : b + 1].cpu(), *history).reshape(1, 32, 1, 64)
+        torch.testing.assert_close(out[b : b + 1].cpu().double(), fp64, **TOL,
+                                   msg=lambda m: f"seed {seed} row {b} len {lengths[b]}: {m}")
+
+
 def test_long_context_b256_full_length(device):
     """Batch 256 at 2048 tokens (128 blocks each, 15 work items) over a fully shuffled
     40000-block pool -- several rounds of workgroups: rows against the oracle, and a
