@@ -630,6 +630,10 @@ def run_extra(selected: set, steps: int, cpu_seconds: float = 0.0) -> dict:
         extra["long_context_b256"] = run_long_context(max(5, steps // 5), 2, cpu_seconds)
         torch.cuda.empty_cache()
         print(f"long context: {extra['long_context_b256']}", file=sys.stderr, flush=True)
+    if "decode_step" in selected:
+        extra["decode_step_b128"] = run_decode_step(max(10, steps // 2), 3)
+        torch.cuda.empty_cache()
+        print(f"decode step: {extra['decode_step_b128']}", file=sys.stderr, flush=True)
     if "prefill" in selected:
         extra["prefill_2048"] = run_prefill(5)
         torch.cuda.empty_cache()
@@ -638,10 +642,6 @@ def run_extra(selected: set, steps: int, cpu_seconds: float = 0.0) -> dict:
         extra["serving"] = run_serving()
         torch.cuda.empty_cache()
         print(f"serving: {extra['serving']}", file=sys.stderr, flush=True)
-    if "decode_step" in selected:
-        extra["decode_step_b128"] = run_decode_step(max(10, steps // 2), 3)
-        torch.cuda.empty_cache()
-        print(f"decode step: {extra['decode_step_b128']}", file=sys.stderr, flush=True)
     return extra
 
 
