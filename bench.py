@@ -323,6 +323,55 @@ def cpu_append_baseline(w: workloads.PromptAppend, table: Sequence[int], seconds
     }
 
 
+def run_single_decode(calls: int = 200) -> dict:
+    """The single-sequence decode case: one query [1, 32, 64] over 128 cached tokens (8
+    blocks of a random table in a NaN-poisoned 64-block pool), one layer. Latency-bound
+    (139 KB of K/V, Q and O), so it is reported as the average duration of one
+    pc_paged_decode_attn call, `calls` calls replayed back to back as one graph."""
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device).manual_seed(1)
+    pool = torch.full((LAYERS, 2, 64, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    table = torch.randperm(64, generator=torch.Generator().manual_seed(1))[:8].to(torch.int32)
+    lengths = np.array([128], dtype=np.int32)
+    for i, block in enumerate(table.tolist()):
+        pool[:, :, block] = torch.randn((LAYERS, 2, 16, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    query = torch.randn((1, 32, 64), dtype=torch.float16, device=device, generator=gen)
+    out = torch.empty_like(query)
+    lib = _hip.load()
+    plan = torch.from_numpy(_hip.decode_plan(lengths, table.numpy()[None])).to(device)
+    lens = torch.from_numpy(lengths).to(device)
+    workspace = torch.empty(256, dtype=torch.uint8, device=device)
+
+    def call() -> None:
+        status = lib.pc_paged_decode_attn(
+            out.data_ptr(), query.data_ptr(), pool.data_ptr(), 64, 0, lens.data_ptr(), 1, 8, plan.data_ptr(),
+            plan.shape[0], workspace.data_ptr(), torch.cuda.current_stream(device).cuda_stream,
+        )
+        if status:
+            raise RuntimeError(lib.pc_last_error().decode())
+
+    call()
+    torch.cuda.synchronize(device)
+    if not torch.isfinite(out).all():
+        raise RuntimeError("single decode produced non-finite output")
+
+    def calls_fn() -> None:
+        for _ in range(calls):
+            call()
+
+    graph = _captured(calls_fn, device)
+    graph.replay()
+    total_ms = _timed(graph.replay, 1, device)
+    nbytes = attention_bytes(lengths)
+    us = total_ms / calls * 1e3
+    return {
+        "workload": "one sequence, 128 cached tokens on a random 8-block table of a 64-block pool, one layer",
+        "us_per_call": round(us, 3),
+        "bytes_per_call": int(nbytes),
+        "gbps": round(nbytes / (us / 1e6) / 1e9, 2),
+    }
+
+
 def run_prompt_append(steps: int, cpu_seconds: float = 0.0) -> dict:
     """Prompt KV append: one 2048-token prompt's K and V (22 layers, N(0, 1) fp16) into a
     4096-block pool whose free list is in seeded random order with 30% of it held by 10
@@ -634,6 +683,9 @@ def run_extra(selected: set, steps: int, cpu_seconds: float = 0.0) -> dict:
     """The workloads beside the headline, each reported as its own object (with a CPU
     baseline of about `cpu_seconds` where the workload has one; 0 = none)."""
     extra = {}
+    if "single_decode" in selected:
+        extra["single_decode_c1"] = run_single_decode()
+        print(f"single decode: {extra['single_decode_c1']}", file=sys.stderr, flush=True)
     if "prompt_append" in selected:
         extra["prompt_append"] = run_prompt_append(max(10, steps), cpu_seconds)
         torch.cuda.empty_cache()
@@ -665,8 +717,9 @@ def main() -> int:
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-graph", action="store_true", help="launch from Python instead of replaying a HIP graph")
-    parser.add_argument("--workloads", default="attention,prompt_append,long_context,prefill,decode_step,serving",
-                        help="comma list: attention (the headline; without it only the others run, as a diagnostic line), prompt_append (2048-token prompt into a "
+    parser.add_argument("--workloads", default="attention,single_decode,prompt_append,long_context,prefill,decode_step,serving",
+                        help="comma list: attention (the headline; without it only the others run, as a diagnostic line), single_decode "
+                        "(one 128-token sequence: call latency), prompt_append (2048-token prompt into a "
                         "fragmented pool), long_context (batch 256 x 2048, append + attention), prefill (one 2048-token "
                         "prompt through the model), decode_step (full TinyLlama-architecture step, batch 128), serving "
                         "(continuous batching of 128 requests)")
@@ -685,7 +738,7 @@ def main() -> int:
     if args.calibrate_copy_mib > 0:
         calibration_copy(args.calibrate_copy_mib, torch.device("cuda:0"))
     selected = {name.strip() for name in args.workloads.split(",")}
-    unknown = selected - {"attention", "prompt_append", "long_context", "prefill", "decode_step", "serving"}
+    unknown = selected - {"attention", "single_decode", "prompt_append", "long_context", "prefill", "decode_step", "serving"}
     if unknown:
         print(f"unknown workloads {sorted(unknown)}", file=sys.stderr)
         return 2
