@@ -581,8 +581,14 @@ def test_gather_block_tables_follows_staged_tables_and_caches_per_state():
         assert staged[0, :2].tolist() == [allocator.block_table(requests[0])[0], allocator._free_blocks[-1]]
         again = allocator.gather_block_tables(requests, layer_index=0)
         assert again[0] is staged  # the 22 layers of a step share one table upload
+        # the cached lookup still refuses a layer that is not written yet
+        with pytest.raises(RuntimeError, match="unwritten"):
+            allocator.gather_block_tables(requests, layer_index=1)
+        with pytest.raises(RuntimeError, match="unwritten"):
+            allocator.gather_block_tables(requests[::-1], layer_index=3)
         for layer in range(1, 22):
             allocator.write_decode_layers(requests, layer, torch.zeros(2, 4, 64, dtype=torch.float16), torch.zeros(2, 4, 64, dtype=torch.float16))
+            assert allocator.gather_block_tables(requests, layer_index=layer)[0] is staged
     committed, committed_lengths = allocator.gather_block_tables(requests, layer_index=0)
     assert committed_lengths.tolist() == [17, 41]
     assert committed[0, :2].tolist() == list(allocator.block_table(requests[0]))
