@@ -36,7 +36,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-from pagedcore_amd import _hip, workloads  # noqa: E402
+from pagedcore_amd import _hip  # noqa: E402
+from tests import workloads  # noqa: E402
+from tests.support import fragmented_decode_cache  # noqa: E402
 
 LAYERS = 22
 PEAK_HBM_GBPS = 8000.0
@@ -534,34 +536,19 @@ def run_decode_step(steps: int, warmup: int) -> dict:
     pc_paged_decode_attn) launches over the same inputs as a graph of their own (the
     appended rows go to a scratch pool so the cache is not disturbed)."""
     from pagedcore_amd import decoder as dec
-    from pagedcore_amd.engine_types import KVReservation, RequestId
-    from pagedcore_amd.kv_cache import KVAllocator
 
     device = torch.device("cuda:0")
     batch = 128
     rng = workloads.rng(20261205)
     top = 2048 - steps - warmup - 1
     lengths = rng.integers(256, top + 1, size=batch)
-    need = int(((lengths + steps + warmup + 1 + 15) // 16).sum())
-    num_blocks = need + 256
     weights = dec.random_weights(device=device, seed=20261205)
-    pool = torch.empty((LAYERS, 2, num_blocks, 16, 4, 64), dtype=torch.float16, device=device)
-    allocator = KVAllocator(pool)
-    requests = tuple(RequestId(f"seq{i}") for i in range(batch))
-    for request, length in zip(requests, lengths):
-        allocator.create(KVReservation(request, min(128, int((length + steps + warmup + 1 + 15) // 16))))
-    gen = torch.Generator(device=device).manual_seed(5)
-    filled = np.zeros(batch, dtype=np.int64)
     # Appends of up to 256 tokens, requests in a fresh random order each round: every
     # request's blocks end up interleaved with the others' (a fragmented pool).
-    while (filled < lengths).any():
-        for row in rng.permutation(batch):
-            count = int(min(256, lengths[row] - filled[row]))
-            if count > 0:
-                key = torch.randn((LAYERS, count, 4, 64), dtype=torch.float16, device=device, generator=gen)
-                value = torch.randn((LAYERS, count, 4, 64), dtype=torch.float16, device=device, generator=gen)
-                allocator.append(requests[row], key, value)
-                filled[row] += count
+    allocator, requests = fragmented_decode_cache(device, batch, lengths, steps + warmup + 1, seed=5)
+    pool = allocator.pool
+    num_blocks = int(pool.shape[2])
+    gen = torch.Generator(device=device).manual_seed(5)
     graph = dec.DecodeGraph(weights, allocator, batch)
     ids = torch.randint(0, 32000, (batch, 1), device=device, generator=gen)
     state = {"ids": ids}

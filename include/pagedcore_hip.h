@@ -103,7 +103,8 @@ int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks);
  *    sequence's last block: its last id), 0, 0, 0},
  * dealing sequences (longest first) to 8 bins of balanced item counts so that all items of
  * a sequence run on one XCD; bins are interleaved record by record and padded with records
- * whose sequence is -1. Returns the record count, or -pc_status on invalid arguments or if
+ * whose sequence is -1. Returns the record count, or -pc_status on invalid arguments
+ * (including a context length above 16 * max_blocks: its table cannot hold it) or if
  * `capacity` is too small; pc_attn_plan_capacity() always suffices (-1 on invalid
  * arguments).
  *

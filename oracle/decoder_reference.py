@@ -4,7 +4,9 @@ Op for op with src/pagedcore/dense.py and the contiguous forward of
 src/pagedcore/decoder.py:202-240, in torch on the CPU, so that the GPU decode step and
 paged prefill can be checked against "the contiguous FP32 decode" the reference's own
 paged-decode test uses as its expectation (tests/unit/test_decoder.py:144-164:
-decode(..., fp32_attention=True), logits within 5e-3, cached K/V within 2e-3).
+decode(..., fp32_attention=True), logits within 5e-3, cached K/V within 2e-3), and the
+greedy loop of generate (src/pagedcore/decoder.py:70-100) as the expectation of the
+continuous-batching worker.
 
 Weights are any object with the reference's field names (embedding, layers, final_norm,
 lm_head; per layer input_norm, q_proj, k_proj, v_proj, o_proj, post_attention_norm,
@@ -16,7 +18,10 @@ tests/unit/test_decoder.py:78-105, atol=rtol=5e-3); decode logits against the sa
 full-sequence logits; closed forms for RoPE (position 0 is the identity, a rotation keeps
 each (d, d+32) pair's norm, the fp32 rotation makes q.k depend only on the position
 difference) and for RMSNorm (constant rows); planted mistakes (K not rotated, V rotated,
-the rotate-half sign flipped, the 8-head grouping transposed) fail the transformers check.
+the rotate-half sign flipped, the 8-head grouping transposed) fail the transformers check;
+generate's stream against a transformers greedy loop, and its stopping rules (EOS
+selected but not emitted, EOS winning at the limit, ignore_eos, the number of decode
+calls) against scripted logits, with planted rule mistakes that those cases catch.
 """
 
 from __future__ import annotations
@@ -151,6 +156,45 @@ def prefill(input_ids: Tensor, weights) -> Tuple[Tensor, KVCache]:
 def decode_fp32(input_ids: Tensor, cache: KVCache, weights) -> Tuple[Tensor, KVCache]:
     """decoder.py:138-153 with fp32_attention=True: one token [1, 1] after the cache."""
     return forward(input_ids, weights, cache, fp32_attention=True)
+
+
+@torch.inference_mode()
+def decode(input_ids: Tensor, cache: KVCache, weights) -> Tuple[Tensor, KVCache]:
+    """decoder.py:138-153 with fp32_attention=False (what generate uses): one token [1, 1]
+    after the cache, fp16 dense attention."""
+    return forward(input_ids, weights, cache)
+
+
+EOS_TOKEN_ID = 2  # reference src/pagedcore/decoder.py:94
+
+
+@torch.inference_mode()
+def generate(input_ids: Tensor, weights, *, max_new_tokens: int = 128, ignore_eos: bool = False):
+    """decoder.py:70-100: single-sequence greedy generation with the contiguous cache.
+
+    Returns (greedy_ids, emitted_ids, finish_reason) with finish_reason "eos" or "length".
+    The token of step s is the argmax of the last position's logits; it is selected before
+    the stop test, so a stopping EOS is in greedy_ids and not in emitted_ids, and EOS wins
+    when it is selected at the output limit; decode runs only while another token is due
+    (max_new_tokens - 1 decode calls at most)."""
+    if type(max_new_tokens) is not int or not 1 <= max_new_tokens <= 256:
+        raise ValueError("max_new_tokens must be an integer from 1 to 256")
+    if type(ignore_eos) is not bool:
+        raise ValueError("ignore_eos must be a boolean")
+    if input_ids.ndim != 2 or input_ids.shape[0] != 1:
+        raise ValueError("input_ids must be int64 [1, tokens]")
+    if input_ids.shape[1] + max_new_tokens > 2048:
+        raise ValueError("prompt tokens plus requested output must not exceed 2048")
+    logits, cache = prefill(input_ids, weights)
+    selected: List[int] = []
+    for step in range(max_new_tokens):
+        token = logits[:, -1:].argmax(dim=-1)
+        selected.append(int(token.item()))
+        if selected[-1] == EOS_TOKEN_ID and not ignore_eos:
+            return tuple(selected), tuple(selected[:-1]), "eos"
+        if step + 1 < max_new_tokens:
+            logits, cache = decode(token, cache, weights)
+    return tuple(selected), tuple(selected), "length"
 
 
 def pool_layout(cache: KVCache) -> Tuple[Tensor, Tensor]:

@@ -219,8 +219,11 @@ struct AttnArgs {
   int layer, batch, max_blocks, max_items;
 };
 
+// Blocks holding `len` tokens, without the int32 overflow of len + 15.
+__device__ __host__ __forceinline__ int blocks_of(int len) { return len / kSlots + (len % kSlots != 0); }
+
 __device__ __forceinline__ int items_of(int len, int max_blocks) {
-  return len > 0 ? (min((len + kSlots - 1) / kSlots, max_blocks) + kItemBlocks - 1) / kItemBlocks : 0;
+  return len > 0 ? (min(blocks_of(len), max_blocks) + kItemBlocks - 1) / kItemBlocks : 0;
 }
 
 // Reduce-scatter of a PV tile pair over the wave halves: lanes < 32 get x[l] + x[l + 32] / 2^18,
@@ -366,7 +369,7 @@ __global__ __launch_bounds__(kItemThreads) __attribute__((amdgpu_waves_per_eu(6,
   int32_t ids[kSubBlocks];
 #pragma unroll
   for (int t = 0; t < kSubBlocks; ++t) ids[t] = s == 0 ? r[4 + t] : (s == 1 ? r[4 + kSubBlocks + t] : r[4 + 2 * kSubBlocks + t]);
-  const int nblk = min((len + kSlots - 1) / kSlots, a.max_blocks);
+  const int nblk = min(blocks_of(len), a.max_blocks);
   const int count = min(kItemBlocks, nblk - item * kItemBlocks);  // blocks of this item, >= 1
   const int nsub = (count + kSubBlocks - 1) / kSubBlocks;
   const int first = item * kItemBlocks + s * kSubBlocks;          // first block of this wave
@@ -621,14 +624,19 @@ int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, i
   // the longest are padded with empty records.
   std::vector<int32_t> order;
   order.reserve(batch);
-  for (int32_t b = 0; b < batch; ++b)
+  for (int32_t b = 0; b < batch; ++b) {
+    if (context_lens[b] > static_cast<int64_t>(max_blocks) * kSlots) {
+      return -set_error(PC_ERR_ARGUMENT, "context length %d of sequence %d exceeds its %d-block table", context_lens[b], b,
+                        max_blocks);
+    }
     if (context_lens[b] > 0) order.push_back(b);
+  }
   std::stable_sort(order.begin(), order.end(), [&](int32_t x, int32_t y) { return context_lens[x] > context_lens[y]; });
   std::vector<std::vector<int32_t>> bins(kPlanBins);
   std::vector<int64_t> load(kPlanBins, 0);
   for (int32_t b : order) {
     const int32_t len = context_lens[b];
-    const int32_t nblk = std::min((len + kSlots - 1) / kSlots, max_blocks);
+    const int32_t nblk = blocks_of(len);  // <= max_blocks, checked above
     const int32_t nitems = (nblk + kItemBlocks - 1) / kItemBlocks;
     const int bin = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
     load[bin] += nitems;

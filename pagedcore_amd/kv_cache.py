@@ -772,19 +772,15 @@ class KVAllocator:
         self._decode_slot_cache.clear()
 
     def _check_staged_state(self, request_ids: Optional[Sequence[RequestId]] = None) -> None:
-        """Accounting check of the per-layer calls of a decode step.
-
-        Outside a staged decode this is the full _assert_accounting. Inside one, every
-        mutation through this API raises, the staged tables and lengths of the step's
-        requests are private copies verified by the full check when the step began, and
-        the commit runs the full check again before anything is published; so calls that
-        only touch the step's requests (request_ids None: the write calls, which look the
-        requests up in the staged set) skip the O(pool) scan, which would otherwise run
-        twice per layer.
-        """
-        appends = self._decode_appends
-        if appends is None or (request_ids is not None and any(r not in appends for r in request_ids)):
-            self._assert_accounting()
+        """Accounting check of the per-layer calls of a decode step: _assert_accounting on
+        every call, inside a staged decode as well, as the reference's write_decode_layer
+        does (src/pagedcore/kv_cache.py:231). A corruption planted between two layer
+        writes therefore raises at the next write, before anything is published. The
+        check is memoised on the bookkeeping containers' mutation counts, so an
+        unchanged state costs a key comparison, not a pool scan. `request_ids` is
+        accepted for the callers' symmetry and does not change the check."""
+        del request_ids
+        self._assert_accounting()
 
     def _check_mutation(self) -> None:
         self._check_worker()

@@ -103,6 +103,9 @@ class DecodeWorker:
     decode_paged. `prefill_graph_tokens` does the same for admissions: a prompt of T
     positions replays the PrefillGraph of the smallest size >= T (it computes the last
     position's logits only, all the selection needs); longer prompts run prefill_paged.
+    `vocab_size` (default: rows of `weights.embedding`, when the weights have one) bounds
+    the token ids submit() accepts. A prefill that raises during admission releases the
+    request's reservation and drops it from the active set before the error propagates.
     """
 
     def __init__(
@@ -116,9 +119,15 @@ class DecodeWorker:
         decode: Optional[DecodeFn] = None,
         graph_batch: Union[None, int, Sequence[int]] = None,
         prefill_graph_tokens: Sequence[int] = (),
+        vocab_size: Optional[int] = None,
     ) -> None:
         if type(max_active) is not int or max_active < 1:
             raise ValueError("max_active must be a positive integer")
+        if vocab_size is None:
+            embedding = getattr(weights, "embedding", None)
+            vocab_size = None if embedding is None else int(embedding.shape[0])
+        if vocab_size is not None and (type(vocab_size) is not int or vocab_size < 1):
+            raise ValueError("vocab_size must be a positive integer")
         sizes = () if graph_batch is None else (graph_batch,) if isinstance(graph_batch, int) else tuple(graph_batch)
         if any(type(size) is not int or size < 1 for size in sizes):
             raise ValueError("graph batch sizes must be positive integers")
@@ -131,6 +140,7 @@ class DecodeWorker:
             prefill = prefill or decoder.prefill_paged
             decode = decode or decoder.decode_paged
         self._weights = weights
+        self._vocab = vocab_size
         self._allocator = allocator
         self._max_active = max_active
         self._eos = eos_token_id
@@ -149,8 +159,12 @@ class DecodeWorker:
     # -- queue -----------------------------------------------------------------------------
 
     def submit(self, request: GenerationRequest) -> None:
+        """Queue a request. Token ids are checked against the model's vocabulary here, on
+        the host: an id past the embedding table would be an out-of-bounds device read."""
         if request.request_id in self._known:
             raise ValueError("request IDs must be unique")
+        if self._vocab is not None and max(request.input_ids) >= self._vocab:
+            raise ValueError(f"input_ids must be below the vocabulary size {self._vocab}")
         if request.block_credits > self._allocator.pool.shape[2]:
             raise ValueError("request exceeds total KV pool capacity")
         self._known.add(request.request_id)
@@ -231,13 +245,22 @@ class DecodeWorker:
         rid = request.request_id
         self._allocator.create(KVReservation(rid, request.block_credits))
         self._active[rid] = _Active(request)
-        ids = torch.tensor([list(request.input_ids)], dtype=torch.int64, device=self._device())
-        size = next((size for size in self._prompt_sizes if size >= len(request.input_ids)), None)
-        if size is not None:
-            logits = self._prefill_graph_for(size).step(ids, rid)
-        else:
-            logits = self._prefill(ids, self._weights, self._allocator, rid)
-        self._select(rid, int(logits[0, -1].argmax()), emitted)
+        try:
+            ids = torch.tensor([list(request.input_ids)], dtype=torch.int64, device=self._device())
+            size = next((size for size in self._prompt_sizes if size >= len(request.input_ids)), None)
+            if size is not None:
+                logits = self._prefill_graph_for(size).step(ids, rid)
+            else:
+                logits = self._prefill(ids, self._weights, self._allocator, rid)
+            token = int(logits[0, -1].argmax())
+        except BaseException:
+            # A failed admission leaves nothing behind: the request leaves the active set
+            # and its reservation (with any blocks a partial prefill published) is
+            # released, so later iterations decode the others and the credits return.
+            self._active.pop(rid, None)
+            self._allocator.release_all(rid)
+            raise
+        self._select(rid, token, emitted)
 
     def _graph_for(self, size: int):
         graph = self._graphs.get(size)

@@ -30,7 +30,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 
 from oracle import paged_reference as ref  # noqa: E402
-from pagedcore_amd import workloads  # noqa: E402
+from tests import workloads  # noqa: E402
 
 
 def digest(array: np.ndarray) -> str:

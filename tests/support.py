@@ -55,3 +55,30 @@ def cached(allocator: KVAllocator, key: Tensor, value: Tensor, name: str = "atte
     allocator.create(KVReservation(request, (key.shape[1] + 15) // 16))
     allocator.append(request, key, value)
     return request
+
+
+def fragmented_decode_cache(
+    device: torch.device, batch: int, lengths: "np.ndarray", spare_tokens: int, seed: int
+) -> tuple[KVAllocator, tuple[RequestId, ...]]:
+    """The decode-step workload's cache: `batch` requests holding `lengths` tokens of N(0, 1)
+    K/V in a pool sized to their blocks plus `spare_tokens` more positions each (and 256
+    free blocks), filled by appends of up to 256 tokens with the requests in a fresh random
+    order each round, so every request's blocks interleave with the others'."""
+    rng = np.random.default_rng(seed)
+    need = int(((lengths + spare_tokens + 15) // 16).sum())
+    pool = torch.empty((22, 2, need + 256, 16, 4, 64), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    requests = tuple(RequestId(f"seq{i}") for i in range(batch))
+    for request, length in zip(requests, lengths):
+        allocator.create(KVReservation(request, min(128, int((length + spare_tokens + 15) // 16))))
+    gen = torch.Generator(device=device).manual_seed(seed)
+    filled = np.zeros(batch, dtype=np.int64)
+    while (filled < lengths).any():
+        for row in rng.permutation(batch):
+            count = int(min(256, lengths[row] - filled[row]))
+            if count > 0:
+                key = torch.randn((22, count, 4, 64), dtype=torch.float16, device=device, generator=gen)
+                value = torch.randn((22, count, 4, 64), dtype=torch.float16, device=device, generator=gen)
+                allocator.append(requests[row], key, value)
+                filled[row] += count
+    return allocator, requests

@@ -560,6 +560,33 @@ def test_decode_write_failure_discards_the_staged_step():
     assert [allocator.cached_length(request) for request in requests] == [16, 17]
 
 
+@pytest.mark.parametrize("batched", [False, True])
+def test_corruption_planted_mid_step_raises_at_the_next_layer_write(batched):
+    """The reference checks the accounting on every write_decode_layer
+    (src/pagedcore/kv_cache.py:227): a duplicate free block planted between two layer
+    writes raises at the next write, and nothing of the step is published."""
+    writer = CpuCopyWriter()
+    allocator = cpu_allocator(torch.zeros(22, 2, 4, 16, 4, 64, dtype=torch.float16), writer)
+    request = RequestId("x")
+    allocator.create(KVReservation(request, 2))
+    allocator.append(request, *kv_values(16))
+    owned = allocator.block_table(request)[0]
+    key = torch.ones(1, 4, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="owned KV blocks must not be free"):
+        with allocator.append_decode((request,)):
+            for layer in range(22):
+                if layer == 3:
+                    allocator._free_blocks.append(owned)
+                if batched:
+                    allocator.write_decode_layers((request,), layer, key, -key)
+                else:
+                    allocator.write_decode_layer(request, layer, key[0], -key[0])
+    assert writer.calls == 1 + 3  # the prompt append and layers 0..2; layer 3 raised first
+    assert allocator._decode_appends is None
+    allocator._free_blocks.pop()
+    assert allocator.cached_length(request) == 16
+
+
 # --- device tables ---------------------------------------------------------------------------
 
 

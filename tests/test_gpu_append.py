@@ -18,7 +18,8 @@ import pytest
 import torch
 
 from oracle import paged_reference as ref
-from pagedcore_amd import _hip, workloads
+from pagedcore_amd import _hip
+from tests import workloads
 from pagedcore_amd.engine_types import CapacityCounts, KVReservation, RequestId
 from pagedcore_amd.kv_cache import HipKVWriter, KVAllocator
 from tests.support import kv_values

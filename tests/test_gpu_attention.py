@@ -2,8 +2,11 @@
 
 The reference's attention tests (tests/unit/test_attention.py, tests/gpu/test_attention_cuda.py)
 re-run against the HIP path through the unchanged Python API, plus the batched shapes the
-hot path is measured on. Tolerance: max-abs/rel 2e-3 on fp16 outputs (the reference's
-policy), tighter where the reference uses a tighter bound.
+hot path is measured on. Tolerance: max |gpu - expected| <= 2e-3 on the fp16 outputs with
+no relative term (the north star's bound; the reference's own tests use assert_close with
+atol = rtol = 2e-3, which is looser), against both the op-for-op oracle (an fp16 output)
+and FP64 dense attention (compared unrounded); tighter where the reference uses a tighter
+bound. Each check prints the largest error it saw.
 """
 
 from __future__ import annotations
@@ -16,19 +19,47 @@ import pytest
 import torch
 
 from oracle import paged_reference as ref
-from pagedcore_amd import _hip, workloads
+from pagedcore_amd import _hip
+from tests import workloads
 from pagedcore_amd.attention import paged_attention, paged_attention_batch
 from pagedcore_amd.engine_types import CapacityCounts, KVReservation, RequestId
 from pagedcore_amd.kv_cache import KVAllocator
 
 pytestmark = pytest.mark.gpu
 
-TOL = dict(atol=2e-3, rtol=2e-3)
+ATOL = 2e-3  # max-abs bound on fp16 attention outputs; no relative term
 
 
 def _say(*parts) -> None:
     print(*parts, flush=True)
     sys.stdout.flush()
+
+
+def assert_max_abs(got, expected, what: str = "", atol: float = ATOL) -> float:
+    """max |got - expected| <= atol (elementwise, in float64, no relative term); both must
+    be finite. Returns the error."""
+    got64 = got.detach().cpu().double()
+    expected64 = expected.detach().cpu().double().reshape(got64.shape)
+    assert torch.isfinite(got64).all(), f"{what}: non-finite output"
+    assert torch.isfinite(expected64).all(), f"{what}: non-finite expectation"
+    error = (got64 - expected64).abs().max().item() if got64.numel() else 0.0
+    assert error <= atol, f"{what}: max |got - expected| = {error:.3e} > {atol:.1e}"
+    return error
+
+
+class Worst:
+    """Largest oracle / FP64 errors seen by one test, printed at its end."""
+
+    def __init__(self, name: str) -> None:
+        self.name, self.oracle, self.fp64 = name, 0.0, 0.0
+
+    def check(self, got, oracle, fp64, what: str) -> None:
+        if oracle is not None:
+            self.oracle = max(self.oracle, assert_max_abs(got, oracle, f"{what} vs oracle"))
+        self.fp64 = max(self.fp64, assert_max_abs(got, fp64, f"{what} vs fp64"))
+
+    def report(self) -> None:
+        _say(f"{self.name}: max |gpu - oracle| = {self.oracle:.2e}, max |gpu - fp64| = {self.fp64:.2e} (bound {ATOL:.0e})")
 
 
 def test_device_is_gfx950_and_one_hip_runtime_is_mapped(device):
@@ -43,8 +74,8 @@ def test_device_is_gfx950_and_one_hip_runtime_is_mapped(device):
         assert any(_hip.LIBRARY_NAME in line for line in maps)
 
 
-def _fp64_half(query, key, value):
-    return ref.dense_attention_fp64(query, key, value).reshape(1, 32, 1, 64).half()
+def _fp64(query, key, value):
+    return ref.dense_attention_fp64(query, key, value).reshape(1, 32, 1, 64)
 
 
 def _check(query, key, value, *, layer, atol=2e-3, exact=None):
@@ -81,10 +112,12 @@ def _check(query, key, value, *, layer, atol=2e-3, exact=None):
     assert actual.device == query.device and actual.dtype == torch.float16
     assert actual.shape == (1, 32, 1, 64) and not actual.requires_grad
     assert torch.isfinite(actual).all()
-    expected = _fp64_half(query, key[layer], value[layer])
-    torch.testing.assert_close(actual.cpu(), expected, atol=atol, rtol=2e-3)
+    expected = _fp64(query.detach().cpu(), key[layer].cpu(), value[layer].cpu())
     oracle = ref.reference_paged_attention(query.detach().cpu(), pool.cpu(), layer, list(table), tokens)
-    torch.testing.assert_close(actual.cpu(), oracle, atol=atol, rtol=2e-3)
+    worst = Worst(f"{tokens} tokens, layer {layer}")
+    worst.oracle = assert_max_abs(actual, oracle, "vs oracle", atol)
+    worst.fp64 = assert_max_abs(actual, expected, "vs fp64", atol)
+    worst.report()
     if exact is not None:
         assert torch.equal(actual.cpu(), torch.full_like(actual.cpu(), exact) if not callable(exact) else exact())
     assert torch.equal(autocast_actual, actual)
@@ -209,8 +242,9 @@ def test_config1_golden_through_the_c_abi(device):
     _hip.paged_decode_attention(out, query, pool, w.layer, tables, lens)
     torch.cuda.synchronize()
     expected = torch.from_numpy(golden["expected_fp64"]).reshape(1, 32, 64)
-    torch.testing.assert_close(out.cpu().double(), expected, atol=2e-3, rtol=2e-3)
-    torch.testing.assert_close(out.cpu(), expected.half(), **TOL)
+    worst = Worst("config 1 golden")
+    worst.check(out, None, expected, "config 1")
+    worst.report()
 
 
 def _random_pool(device, num_blocks, seed):
@@ -230,9 +264,9 @@ def _oracle_rows(pool, layer, w, queries, rows):
         q = queries[b : b + 1].reshape(1, 32, 1, 64).cpu()
         out[b] = (
             ref.reference_paged_attention(q, sub, layer, list(range(len(table))), length),
-            ref.dense_attention_fp64(q, *ref.gather_history(sub, layer, list(range(len(table))), length))
-            .reshape(1, 32, 1, 64)
-            .half(),
+            ref.dense_attention_fp64(q, *ref.gather_history(sub, layer, list(range(len(table))), length)).reshape(
+                1, 32, 1, 64
+            ),
         )
     return out
 
@@ -263,10 +297,10 @@ def test_batched_decode_b64_matches_oracle(device, order):
     )
     torch.cuda.synchronize()
     expected = _oracle_rows(pool, layer, w, queries, range(w.batch))
+    worst = Worst(f"batch 64 ({order} plan)")
     for b, (oracle, fp64) in expected.items():
-        got = out[b : b + 1].reshape(1, 32, 1, 64).cpu()
-        torch.testing.assert_close(got, oracle, **TOL, msg=lambda m: f"row {b} len {w.lengths[b]}: {m}")
-        torch.testing.assert_close(got, fp64, **TOL, msg=lambda m: f"row {b} len {w.lengths[b]} fp64: {m}")
+        worst.check(out[b : b + 1].reshape(1, 32, 1, 64), oracle, fp64, f"row {b} len {w.lengths[b]}")
+    worst.report()
 
 
 def test_work_item_boundaries_match_oracle(device):
@@ -293,10 +327,10 @@ def test_work_item_boundaries_match_oracle(device):
     _hip.paged_decode_attention(out, queries, pool, layer, torch.from_numpy(tables).to(device),
                                 torch.from_numpy(lengths).to(device))
     torch.cuda.synchronize()
+    worst = Worst("work-item boundaries")
     for b, (oracle, fp64) in _oracle_rows(pool, layer, w, queries, range(len(lengths))).items():
-        got = out[b : b + 1].reshape(1, 32, 1, 64).cpu()
-        torch.testing.assert_close(got, oracle, **TOL, msg=lambda m: f"row {b} len {lengths[b]}: {m}")
-        torch.testing.assert_close(got, fp64, **TOL, msg=lambda m: f"row {b} len {lengths[b]} fp64: {m}")
+        worst.check(out[b : b + 1].reshape(1, 32, 1, 64), oracle, fp64, f"row {b} len {lengths[b]}")
+    worst.report()
 
 
 @pytest.mark.parametrize("seed", [101, 202, 303, 404])
@@ -322,6 +356,7 @@ def test_random_batches_through_the_allocator_match_fp64(device, seed):
     query = torch.randn(batch, 32, 1, 64, dtype=torch.float16, device=device, generator=gen)
     out = paged_attention_batch(query, allocator, requests, layer_index=layer)
     torch.cuda.synchronize()
+    worst = Worst(f"random batch seed {seed}")
     for b, request in enumerate(requests):
         table = list(allocator.block_table(request))
         index = torch.tensor(table, dtype=torch.long, device=device)
@@ -329,18 +364,55 @@ def test_random_batches_through_the_allocator_match_fp64(device, seed):
         sub[layer] = pool[layer].index_select(1, index).cpu()
         history = ref.gather_history(sub, layer, list(range(len(table))), int(lengths[b]))
         fp64 = ref.dense_attention_fp64(query[b : b + 1].cpu(), *history).reshape(1, 32, 1, 64)
-        torch.testing.assert_close(out[b : b + 1].cpu().double(), fp64, **TOL,
-                                   msg=lambda m: f"seed {seed} row {b} len {lengths[b]}: {m}")
+        worst.check(out[b : b + 1], None, fp64, f"seed {seed} row {b} len {lengths[b]}")
+    worst.report()
+
+
+def _fp64_all_rows(pool, layer, tables, lengths, queries, chunk=32):
+    """FP64 dense attention of every row over its gathered history (rows batched, the
+    history masked past each row's length): [batch, 32, 64] float64 on the CPU."""
+    batch = queries.shape[0]
+    out = torch.empty((batch, 32, 64), dtype=torch.float64)
+    for lo in range(0, batch, chunk):
+        hi = min(batch, lo + chunk)
+        lens = torch.as_tensor(np.asarray(lengths[lo:hi], dtype=np.int64))
+        width = int((lens.max() + 15) // 16)
+        ids = torch.as_tensor(np.asarray(tables[lo:hi, :width], dtype=np.int64)).clamp(0, pool.shape[2] - 1)
+        k, v = (pool[layer, kind].index_select(0, ids.reshape(-1).to(pool.device)).cpu() for kind in (0, 1))
+        k = k.reshape(hi - lo, width * 16, 4, 64).permute(0, 2, 1, 3).double()  # [rows, 4, T, 64]
+        v = v.reshape(hi - lo, width * 16, 4, 64).permute(0, 2, 1, 3).double()
+        q = queries[lo:hi].cpu().double().reshape(hi - lo, 4, 8, 64)
+        scores = torch.matmul(q, k.transpose(-1, -2).contiguous()) / 8.0  # [rows, 4, 8, T]
+        mask = torch.arange(width * 16)[None, :] >= lens[:, None]
+        scores.masked_fill_(mask[:, None, None, :], float("-inf"))
+        out[lo:hi] = torch.matmul(torch.softmax(scores, dim=-1), v).reshape(hi - lo, 32, 64)
+    return out
 
 
 def test_long_context_b256_full_length(device):
-    """Batch 256 at 2048 tokens (128 blocks each, 15 work items) over a fully shuffled
-    40000-block pool -- several rounds of workgroups: rows against the oracle, and a
-    shuffled plan giving the same bits."""
-    _say("b256 long context")
+    """The long-context workload as one step of one layer: batch 256, each sequence 2047
+    cached tokens on 128 blocks of a fully shuffled 40000-block pool; pc_kv_append writes
+    every sequence's new token (slot 2047), then attention runs over 2048 tokens (15 work
+    items each, several rounds of workgroups). The appended rows are bit-exact, every row
+    is within 2e-3 of FP64, sampled rows within 2e-3 of the op-for-op oracle, and a
+    shuffled plan gives the same bits."""
+    _say("b256 long context: append + attention")
     w = workloads.batched_decode(batch=256, num_blocks=40000, fixed_length=2048, seed=44)
     pool = _random_pool(device, w.num_blocks, 12)
     layer = 21
+    gen = torch.Generator(device=device).manual_seed(21)
+    new_key = torch.randn((1, w.batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    new_value = torch.randn((1, w.batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    last = torch.from_numpy(w.tables[:, 127].astype(np.int64))
+    slots = (last * 16 + 15).to(device)
+    before = pool[layer, :, last.to(device)].clone()  # [2, 256, 16, 4, 64]
+    _hip.kv_append(pool, layer, new_key, new_value, slots)
+    after = pool[layer, :, last.to(device)]
+    torch.cuda.synchronize()
+    assert torch.equal(after[0, :, 15].view(torch.int16), new_key[0].view(torch.int16))
+    assert torch.equal(after[1, :, 15].view(torch.int16), new_value[0].view(torch.int16))
+    assert torch.equal(after[:, :, :15].view(torch.int16), before[:, :, :15].view(torch.int16))
+
     queries = torch.from_numpy(w.queries(layer)).to(device)
     tables = torch.from_numpy(w.tables).to(device)
     lens = torch.from_numpy(w.lengths).to(device)
@@ -352,11 +424,14 @@ def test_long_context_b256_full_length(device):
         results[order] = out
     torch.cuda.synchronize()
     assert torch.equal(results["binned"], results["shuffled"])
-    expected = _oracle_rows(pool, layer, w, queries, [0, 1, 127, 255])
-    for b, (oracle, fp64) in expected.items():
-        got = results["binned"][b : b + 1].reshape(1, 32, 1, 64).cpu()
-        torch.testing.assert_close(got, oracle, **TOL)
-        torch.testing.assert_close(got, fp64, **TOL)
+    got = results["binned"]
+    worst = Worst("b256 x 2048 after append")
+    fp64 = _fp64_all_rows(pool, layer, w.tables, w.lengths, queries)
+    for b in range(w.batch):
+        worst.check(got[b], None, fp64[b], f"row {b}")
+    for b, (oracle, _) in _oracle_rows(pool, layer, w, queries, [0, 1, 63, 64, 127, 128, 200, 255]).items():
+        worst.oracle = max(worst.oracle, assert_max_abs(got[b : b + 1].reshape(1, 32, 1, 64), oracle, f"row {b} vs oracle"))
+    worst.report()
 
 
 def test_plan_order_and_graph_replays_are_invisible(device):
@@ -402,10 +477,10 @@ def test_plan_order_and_graph_replays_are_invisible(device):
         torch.cuda.synchronize()
         assert torch.equal(eager[live], first[live])
     w.lengths = lengths
+    worst = Worst("plan order and graph replays")
     for b, (oracle, fp64) in _oracle_rows(pool, 9, w, queries, [0, 1, 2, 3, 4, 5, 40]).items():
-        got = first[b : b + 1].reshape(1, 32, 1, 64).cpu()
-        torch.testing.assert_close(got, oracle, **TOL)
-        torch.testing.assert_close(got, fp64, **TOL)
+        worst.check(first[b : b + 1].reshape(1, 32, 1, 64), oracle, fp64, f"row {b}")
+    worst.report()
 
 
 def test_cached_scratch_survives_changing_shapes(device):
@@ -420,8 +495,10 @@ def test_cached_scratch_survives_changing_shapes(device):
             out, queries, pool, layer, torch.from_numpy(w.tables).to(device), torch.from_numpy(w.lengths).to(device)
         )
         torch.cuda.synchronize()
+        worst = Worst(f"scratch reuse batch {batch} hi {hi}")
         for b, (oracle, fp64) in _oracle_rows(pool, layer, w, queries, range(batch)).items():
-            torch.testing.assert_close(out[b : b + 1].reshape(1, 32, 1, 64).cpu(), oracle, **TOL)
+            worst.check(out[b : b + 1].reshape(1, 32, 1, 64), oracle, fp64, f"row {b}")
+        worst.report()
 
 
 def test_constant_values_return_the_constant(device):

@@ -670,3 +670,221 @@ def test_worker_streams_equal_each_request_generated_alone(device, graph_batch, 
         assert got.greedy_ids == ids and got.finish_reason == reason, request.request_id
     counts = allocator.capacity()
     assert counts.owned_blocks == 0 and counts.reserved_blocks == 0 and counts.active_slots == 0
+
+
+# ---------------------------------------------------------------------------------------
+# Reference decoder cases re-expressed on the GPU path
+# ---------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_decode_at_the_last_context_position(device, use_graph):
+    """tests/unit/test_decoder.py:359-378: 2047 cached positions; decode writes position 2047
+    (block 127, slot 15) and the logits match the contiguous fp32 decode; the next decode
+    is refused with ValueError and changes nothing (counts, length, pool bytes)."""
+    weights = _synthetic(device)
+    host_weights = _cpu(weights)
+    pool = torch.zeros(22, 2, 128, 16, 4, 64, dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    request = RequestId("last")
+    allocator.create(KVReservation(request, 128))
+    gen = torch.Generator(device=device).manual_seed(4)
+    history = torch.randn(22, 2047, 4, 64, dtype=torch.float16, device=device, generator=gen)
+    allocator.append(request, history, -history)
+    cache = _pool_cache(allocator, request)
+    step = dec.DecodeGraph(weights, allocator, 1).step if use_graph else (
+        lambda ids, rids: dec.decode_paged(ids, weights, allocator, rids))
+    logits = step(torch.tensor([[3]], device=device), (request,))
+    torch.cuda.synchronize()
+    assert logits.shape == (1, 1, 31) and torch.isfinite(logits).all()
+    assert allocator.cached_length(request) == 2048
+    expected, new_cache = dref.decode_fp32(torch.tensor([[3]]), cache, host_weights)
+    torch.testing.assert_close(logits.cpu(), expected, atol=5e-3, rtol=5e-3)
+    block = allocator.block_table(request)[127]
+    got = _pool_cache(allocator, request)
+    for layer in range(22):
+        for kind in range(2):
+            assert torch.equal(got[layer][kind][:, :, :2047], cache[layer][kind])
+            torch.testing.assert_close(got[layer][kind][:, :, 2047], new_cache[layer][kind][:, :, 2047], atol=2e-3, rtol=0)
+    assert torch.isfinite(pool[:, :, block, 15]).all()
+    counts = allocator.capacity()
+    before = pool.clone()
+    with pytest.raises(ValueError, match="2047"):
+        step(torch.tensor([[5]], device=device), (request,))
+    assert allocator.capacity() == counts
+    assert allocator.cached_length(request) == 2048
+    assert torch.equal(pool.view(torch.int16), before.view(torch.int16))
+
+
+@pytest.mark.parametrize("tokens", [1, 15, 16, 17, 49])
+def test_prefill_writes_absolute_positions_to_reused_fragmented_pages(device, tokens):
+    """tests/unit/test_decoder.py:440-493: three one-block requests hold sentinel K/V, the
+    first and last are released, and the prompt then gets the table (2, 0, 3, 4): its
+    positions land in reused, out-of-order blocks. Logits against the contiguous prefill,
+    layer-0 K/V within 2e-3 (every layer as accurate as the CPU fp16 forward), the
+    reference's counts, NaN poison kept in the tail slots, and every other block (the
+    retained sentinel and the free blocks' old bytes) unchanged."""
+    weights = _synthetic(device)
+    host_weights = _cpu(weights)
+    exact = _fp32(host_weights)
+    pool = torch.full((22, 2, 6, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    for name in ("released_first", "retained", "released_last"):
+        request = RequestId(name)
+        allocator.create(KVReservation(request, 1))
+        key = torch.full((22, 16, 4, 64), -100.0, dtype=torch.float16, device=device)
+        allocator.append(request, key, -key)
+    allocator.release_all(RequestId("released_first"))
+    allocator.release_all(RequestId("released_last"))
+    request = RequestId("prompt")
+    blocks = (tokens + 15) // 16
+    allocator.create(KVReservation(request, blocks))
+    before = pool.clone()
+    pointer = pool.untyped_storage().data_ptr()
+    ids = torch.arange(tokens)[None] % 31
+    expected_logits, expected_cache = dref.prefill(ids, host_weights)
+    exact_logits, exact_cache = dref.forward(ids, exact)
+
+    logits = dec.prefill_paged(ids.to(device), weights, allocator, request)
+    torch.cuda.synchronize()
+
+    torch.testing.assert_close(logits.cpu(), expected_logits, atol=5e-3, rtol=5e-3)
+    _as_accurate(logits, expected_logits, exact_logits)
+    assert logits.dtype == torch.float16 and not logits.requires_grad
+    assert pool.untyped_storage().data_ptr() == pointer
+    assert allocator.block_table(request) == (2, 0, 3, 4)[:blocks]
+    assert allocator.cached_length(request) == tokens
+    assert allocator.capacity() == CapacityCounts(6, 5 - blocks, blocks + 1, blocks + 1, 2, tokens + 16)
+    got = _pool_cache(allocator, request)
+    for layer in range(22):
+        for kind in range(2):
+            if layer == 0:
+                torch.testing.assert_close(got[0][kind], expected_cache[0][kind], atol=2e-3, rtol=0)
+            _as_accurate(got[layer][kind], expected_cache[layer][kind], exact_cache[layer][kind])
+    for logical, physical in enumerate(allocator.block_table(request)):
+        valid = min(16, tokens - logical * 16)
+        assert torch.equal(pool[:, :, physical, valid:].view(torch.int16), before[:, :, physical, valid:].view(torch.int16))
+    for physical in set(range(6)) - set(allocator.block_table(request)):
+        assert torch.equal(pool[:, :, physical].view(torch.int16), before[:, :, physical].view(torch.int16))
+    allocator.release_all(request)
+    allocator.release_all(RequestId("retained"))
+    assert allocator.capacity() == CapacityCounts(6, 6, 0, 0, 0, 0)
+
+
+def test_decode_step_b128_at_the_bench_workload(device):
+    """The full decode-step workload (tests/unit/test_decoder.py:114-195 at scale): 22
+    distinct full-size layers (MLP 5632, vocab 32000, N(0, 0.02) weights), batch 128,
+    contexts U{256..2034} of N(0, 1) K/V in a fragmented pool, as the benchmark builds it.
+    One DecodeGraph step, then one eager decode_paged step. For ten rows per step (the
+    shortest and longest, a row whose new token opens a fresh block, one filling the last
+    slot of a block, and random rows) the logits are as close to an fp32 evaluation as the
+    CPU fp16 forward is (started from the GPU's own cache), layer 0's new K/V is within
+    2e-3 of the oracle, and the greedy token agrees wherever the fp32 top-2 margin exceeds
+    that noise. Every row: finite logits, one more cached position, old slots unchanged."""
+    from tests.support import fragmented_decode_cache
+
+    batch = 128
+    rng = np.random.default_rng(20261205)
+    lengths = rng.integers(256, 2035, size=batch)
+    lengths[:4] = [256, 2034, 1024, 1039]  # shortest, longest, fresh block next, last slot next
+    weights = dec.random_weights(device=device, seed=20261205)
+    host_weights = _cpu(weights)
+    exact = _fp32(host_weights)
+    allocator, requests = fragmented_decode_cache(device, batch, lengths, 4, seed=5)
+    pool = allocator.pool
+    scattered = sum(int(np.sum(np.diff(allocator.block_table(r)) != 1)) for r in requests)
+    assert scattered > batch  # the tables really are fragmented
+    graph = dec.DecodeGraph(weights, allocator, batch)
+    checked = [0, 1, 2, 3] + [int(b) for b in rng.choice(np.arange(4, batch), size=6, replace=False)]
+    tokens = torch.from_numpy(rng.integers(0, 32000, size=(batch, 1))).to(device)
+    agreements = 0
+    for name, step in (("graph", graph.step), ("eager", lambda ids, rids: dec.decode_paged(ids, weights, allocator, rids))):
+        old_lengths = [allocator.cached_length(r) for r in requests]
+        caches = {b: _pool_cache(allocator, requests[b]) for b in checked}
+        before = pool.clone()
+        logits = step(tokens, requests)
+        torch.cuda.synchronize()
+        assert logits.shape == (batch, 1, 32000) and torch.isfinite(logits).all(), name
+        written = torch.zeros(pool.shape[2:4], dtype=torch.bool, device=device)
+        for b, request in enumerate(requests):
+            assert allocator.cached_length(request) == old_lengths[b] + 1
+            block, slot = divmod(old_lengths[b], 16)
+            written[allocator.block_table(request)[block], slot] = True
+        assert torch.equal(pool[:, :, ~written].view(torch.int16), before[:, :, ~written].view(torch.int16)), name
+        del before
+        for b in checked:
+            request = requests[b]
+            cpu16, new_cache = dref.decode_fp32(tokens[b : b + 1].cpu(), caches[b], host_weights)
+            fp32 = dref.forward(
+                tokens[b : b + 1].cpu(), exact, [(k.float(), v.float()) for k, v in caches[b]], fp32_attention=True
+            )[0]
+            _as_accurate(logits[b : b + 1], cpu16, fp32)
+            got = _pool_cache(allocator, request)
+            for kind in range(2):
+                torch.testing.assert_close(
+                    got[0][kind][:, :, old_lengths[b]], new_cache[0][kind][:, :, old_lengths[b]], atol=2e-3, rtol=0
+                )
+            top = fp32.flatten().topk(2).values
+            if float(top[0] - top[1]) > 4 * _gap(cpu16, fp32):
+                assert int(logits[b].argmax()) == int(fp32.argmax()), (name, b)
+                agreements += 1
+        print(f"decode step b128 ({name}): {len(checked)} rows checked against the oracle", flush=True)
+        tokens = logits.argmax(-1)
+    assert agreements >= 4  # the argmax condition is not vacuous
+
+
+def _worker_stream_matches_generate(request, result, host_weights, tie: float = 1e-2) -> int:
+    """The worker's greedy stream against the oracle's generate (reference
+    src/pagedcore/decoder.py:70-100). Equal streams and finish reasons pass. A stream may
+    leave the oracle's only at a near-tie: the oracle's own logits at that step, on the
+    common prefix, have a top-2 gap within `tie` (twice the 5e-3 logits tolerance) and the
+    worker chose the runner-up; from there on each worker token must be the oracle's
+    choice (or a near-tie runner-up) given the worker's own prefix. Returns the tie count."""
+    ids = torch.tensor([list(request.input_ids)])
+    greedy, emitted, reason = dref.generate(
+        ids, host_weights, max_new_tokens=request.max_new_tokens, ignore_eos=request.ignore_eos
+    )
+    got = result.greedy_ids
+    if got == greedy:
+        assert result.emitted_ids == emitted and result.finish_reason.value == reason
+        return 0
+    sequence = torch.cat([ids, torch.tensor([list(got[:-1])], dtype=torch.int64)], dim=1)
+    logits = dref.prefill(sequence, host_weights)[0][0, ids.shape[1] - 1 :].float()
+    ties = 0
+    for position, token in enumerate(got):
+        values, indices = logits[position].topk(2)
+        if token == int(indices[0]):
+            continue
+        assert token == int(indices[1]) and float(values[0] - values[1]) <= tie, (request.request_id, position)
+        ties += 1
+    stops = got[-1] == 2 and not request.ignore_eos
+    assert result.finish_reason.value == ("eos" if stops else "length")
+    assert stops or len(got) == request.max_new_tokens
+    assert 2 not in got[:-1] or request.ignore_eos
+    return ties
+
+
+@pytest.mark.parametrize("graph_batch, prompt_graphs", [(None, ()), (3, ()), ((2, 4), (16, 48))])
+def test_worker_streams_match_the_oracle_generate(device, graph_batch, prompt_graphs):
+    """Continuous batching (requests joining and leaving the decode batch every few steps,
+    eager or through padded decode/prefill graphs): every request's tokens and finish
+    reason are those of the oracle's single-sequence greedy generate."""
+    from pagedcore_amd.worker import DecodeWorker, GenerationRequest
+
+    weights = _synthetic(device)
+    host_weights = _cpu(weights)
+    pool = torch.full((22, 2, 48, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    worker = DecodeWorker(weights, allocator, max_active=3, graph_batch=graph_batch, prefill_graph_tokens=prompt_graphs)
+    gen = torch.Generator().manual_seed(13)
+    requests = []
+    for index in range(7):
+        prompt = tuple(int(t) for t in torch.randint(3, 31, (int(torch.randint(1, 40, (1,), generator=gen)),), generator=gen))
+        requests.append(GenerationRequest(RequestId(f"w{index}"), prompt, int(torch.randint(1, 12, (1,), generator=gen)),
+                                          ignore_eos=index % 2 == 0))
+        worker.submit(requests[-1])
+    results = worker.run(max_steps=500)
+    ties = sum(_worker_stream_matches_generate(r, results[r.request_id], host_weights) for r in requests)
+    print(f"worker vs oracle generate: {len(requests)} requests, {ties} near-tie choices", flush=True)
+    counts = allocator.capacity()
+    assert counts.owned_blocks == 0 and counts.reserved_blocks == 0 and counts.active_slots == 0

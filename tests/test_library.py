@@ -108,13 +108,13 @@ def _items_by_enumeration(lengths, tables):
 
 def test_decode_plan_lists_every_item_once_on_one_bin_per_sequence():
     """pc_attn_plan (host code) against a direct enumeration, on ragged lengths including
-    zero-length rows, exact block multiples and lengths clamped by the table width: every
+    zero-length rows, exact block multiples and the full 128-block table width: every
     item appears once, the items of a sequence share record index modulo 8 (one XCD), the
     8 bins' item counts differ by at most one sequence's items, padding records are empty,
     and longer sequences are dealt first."""
     rng = np.random.default_rng(5)
     lengths = rng.integers(0, 2049, size=97).astype(np.int32)
-    lengths[:6] = [0, 1, 16, 17, 2048, 5000]  # 5000 tokens exceed the 128-block width: clamped
+    lengths[:6] = [0, 1, 16, 17, 2048, 2047]
     tables = rng.integers(0, 50000, size=(97, 128)).astype(np.int32)
     plan = _hip.decode_plan(lengths, tables)
     lib = _hip.load()
@@ -160,6 +160,14 @@ def test_decode_plan_rejects_bad_arguments():
     assert lib.pc_attn_plan_capacity(2, 16) == (2 + 8) * 2
     assert lib.pc_attn_plan_capacity(2, 0) == -1
     assert plan(None, None, 0, 16, None, 0) == 0  # empty batch: nothing to plan
+    # a context longer than its table (16 tokens per entry) is refused, not clamped, and the
+    # check does not overflow near INT32_MAX
+    for too_long in (16 * 16 + 1, 2**31 - 1):
+        lens[1] = too_long
+        assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, records.ctypes.data, 64) == -1
+        assert b"exceeds its 16-block table" in lib.pc_last_error()
+    lens[1] = 16 * 16
+    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, records.ctypes.data, 64) == 16
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

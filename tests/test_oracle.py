@@ -294,3 +294,55 @@ def test_planted_fifo_free_list_is_caught():
     lifo.grow_to("b", 16)
     lifo.grow_to("a", 33)
     assert lifo.tables != {"a": [0, 2, 3], "b": [1]}
+
+
+# --- The decode write (kv_cache.py:242-245) ------------------------------------------------
+
+
+def _write_decode_changes(write, length, layer=7, num_blocks=9):
+    """Flat pool indices a decode write changes, for a seeded pool and a 130-entry table
+    (enough entries past the sequence that a misplaced write still lands in the pool)."""
+    rng = np.random.default_rng(length)
+    pool = rng.integers(0, 0x7C00, size=(22, 2, num_blocks, 16, 4, 64), dtype=np.uint16)
+    before = pool.copy()
+    blocks = [int(b) for b in rng.integers(0, num_blocks, size=130)]
+    key = rng.integers(0x7C00, 0x7E00, size=(4, 64), dtype=np.uint16)  # values not in the pool
+    value = key ^ 0x0100
+    write(pool, layer, blocks, length, key, value)
+    changed = np.flatnonzero(pool != before)
+    return pool, blocks, key, value, changed
+
+
+@pytest.mark.parametrize("length", [1, 15, 16, 17, 32, 33, 2047, 2048])
+def test_write_decode_satisfies_the_element_closed_form(length):
+    """The staged token of a length-L sequence goes to position L - 1: element
+    (((layer * 2 + kind) * N + blocks[(L - 1) // 16]) * 16 + (L - 1) % 16) * 256 + h * 64 + d
+    of the flat pool for kind 0 (key) and 1 (value), and nothing else changes."""
+    layer, num_blocks = 7, 9
+    pool, blocks, key, value, changed = _write_decode_changes(ref.reference_write_decode, length, layer, num_blocks)
+    block = blocks[(length - 1) // 16]
+    slot = (length - 1) % 16
+    expected = []
+    for kind in (0, 1):
+        base = (((layer * 2 + kind) * num_blocks + block) * 16 + slot) * 256
+        expected.extend(range(base, base + 256))
+    flat = pool.reshape(-1)
+    assert np.array_equal(flat[np.asarray(expected[:256])], key.reshape(-1))
+    assert np.array_equal(flat[np.asarray(expected[256:])], value.reshape(-1))
+    assert set(changed.tolist()) <= set(expected)  # a byte equal to its old value may not show
+
+
+@pytest.mark.parametrize("shift", [-1, 1])
+def test_planted_write_decode_off_by_one_is_caught(shift):
+    """Writing position L or L - 2 instead of L - 1 fails the closed form at every length."""
+
+    def planted(pool, layer, blocks, length, key, value):
+        ref.reference_write_decode(pool, layer, blocks, length + shift, key, value)
+
+    for length in (2, 16, 17, 33):
+        with pytest.raises(AssertionError):
+            layer, num_blocks = 7, 9
+            pool, blocks, key, value, changed = _write_decode_changes(planted, length, layer, num_blocks)
+            block, slot = blocks[(length - 1) // 16], (length - 1) % 16
+            base = (((layer * 2) * num_blocks + block) * 16 + slot) * 256
+            assert np.array_equal(pool.reshape(-1)[base : base + 256], key.reshape(-1))

@@ -182,3 +182,118 @@ def test_planted_mistakes_fail_the_transformers_check(synthetic, mistake, monkey
         monkeypatch.setattr(dref, "repeat_kv", lambda t: repeat_kv(t).view(t.shape[0], 8, 4, *t.shape[2:]).transpose(1, 2).reshape(t.shape[0], 32, *t.shape[2:]))
     logits, _ = dref.prefill(ids, weights)
     assert not torch.allclose(logits, expected, atol=5e-3, rtol=5e-3)
+
+
+# ---------------------------------------------------------------------------------------
+# generate (reference src/pagedcore/decoder.py:70-100)
+# ---------------------------------------------------------------------------------------
+
+
+def _hf_greedy(model, ids, max_new_tokens, ignore_eos):
+    """A greedy loop over the transformers model (full recompute each step) with the
+    reference's stopping rules."""
+    selected = []
+    sequence = ids
+    for step in range(max_new_tokens):
+        token = int(_hf_logits(model, sequence)[0, -1].argmax())
+        selected.append(token)
+        if token == 2 and not ignore_eos:
+            return tuple(selected), "eos"
+        sequence = torch.cat([sequence, torch.tensor([[token]])], dim=1)
+    return tuple(selected), "length"
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_generate_matches_a_transformers_greedy_loop(synthetic, seed):
+    """The oracle's generate (prefill, then one fp16 decode per further token) selects the
+    same tokens as greedy selection over the transformers model's full-sequence logits."""
+    model, weights = synthetic
+    gen = torch.Generator().manual_seed(seed)
+    ids = torch.randint(3, 31, (1, int(torch.randint(1, 30, (1,), generator=gen))), generator=gen)
+    greedy, emitted, reason = dref.generate(ids, weights, max_new_tokens=12, ignore_eos=seed % 2 == 0)
+    expected, expected_reason = _hf_greedy(model, ids, 12, seed % 2 == 0)
+    assert greedy == expected and reason == expected_reason
+    assert emitted == (greedy[:-1] if reason == "eos" else greedy)
+
+
+class _Scripted:
+    """prefill / decode stand-ins whose last-position logits select script[n] at the n-th
+    selection (the other positions favour another token, so reading the wrong position
+    shows)."""
+
+    def __init__(self, script, vocab=8):
+        self.script, self.vocab, self.decodes = list(script), vocab, 0
+
+    def _logits(self, n, positions):
+        logits = torch.zeros(1, positions, self.vocab, dtype=torch.float16)
+        logits[0, :, (self.script[n] + 1) % self.vocab] = 1.0
+        logits[0, -1] = 0.0
+        logits[0, -1, self.script[n]] = 1.0
+        return logits
+
+    def prefill(self, ids, weights):
+        return self._logits(0, ids.shape[1]), [ids.shape[1]]
+
+    def decode(self, token, cache, weights):
+        self.decodes += 1
+        # the cache counts the forward calls so far; this call feeds the last selection
+        assert token.shape == (1, 1) and int(token) == self.script[len(cache) - 1]
+        return self._logits(len(cache), 1), cache + [len(cache)]
+
+
+@pytest.mark.parametrize(
+    "script,max_new,ignore_eos,expected",
+    [
+        # EOS mid-stream: selected, not emitted; no decode after it
+        ((5, 6, 2, 7), 4, False, ((5, 6, 2), (5, 6), "eos", 2)),
+        # EOS selected exactly at the limit still wins
+        ((5, 6, 2), 3, False, ((5, 6, 2), (5, 6), "eos", 2)),
+        # ignore_eos keeps going through EOS to the limit
+        ((5, 2, 6), 3, True, ((5, 2, 6), (5, 2, 6), "length", 2)),
+        # one token: prefill only, no decode
+        ((7,), 1, False, ((7,), (7,), "length", 0)),
+        # EOS as the very first token
+        ((2, 5), 2, False, ((2,), (), "eos", 0)),
+    ],
+)
+def test_generate_stopping_rules_on_scripted_logits(monkeypatch, script, max_new, ignore_eos, expected):
+    scripted = _Scripted(script)
+    monkeypatch.setattr(dref, "prefill", scripted.prefill)
+    monkeypatch.setattr(dref, "decode", scripted.decode)
+    greedy, emitted, reason = dref.generate(torch.tensor([[1, 3, 4]]), None, max_new_tokens=max_new, ignore_eos=ignore_eos)
+    assert (greedy, emitted, reason, scripted.decodes) == expected
+
+
+def test_generate_validates_like_the_reference():
+    ids = torch.tensor([[1, 2]])
+    for kwargs, needle in (
+        (dict(max_new_tokens=0), "1 to 256"),
+        (dict(max_new_tokens=257), "1 to 256"),
+        (dict(max_new_tokens=True), "1 to 256"),
+        (dict(ignore_eos=1), "boolean"),
+    ):
+        with pytest.raises(ValueError, match=needle):
+            dref.generate(ids, None, **kwargs)
+    with pytest.raises(ValueError, match=r"\[1, tokens\]"):
+        dref.generate(torch.tensor([[1], [2]]), None)
+    with pytest.raises(ValueError, match="2048"):
+        dref.generate(torch.zeros((1, 1950), dtype=torch.int64), None, max_new_tokens=100)
+
+
+@pytest.mark.parametrize("mistake", ["eos_id", "first_position"])
+def test_planted_generate_mistakes_fail_the_scripted_cases(monkeypatch, mistake):
+    """A wrong EOS id, or selecting from the first position instead of the last, changes the
+    scripted streams above."""
+    scripted = _Scripted((5, 6, 2, 7))
+    prefill = scripted.prefill
+    monkeypatch.setattr(dref, "decode", scripted.decode)
+    if mistake == "eos_id":
+        monkeypatch.setattr(dref, "EOS_TOKEN_ID", 3)
+        monkeypatch.setattr(dref, "prefill", prefill)
+    else:
+        monkeypatch.setattr(dref, "prefill", lambda ids, w: (prefill(ids, w)[0][:, :1].flip(1), prefill(ids, w)[1]))
+    try:
+        result = dref.generate(torch.tensor([[1, 3, 4]]), None, max_new_tokens=4)
+    except AssertionError:
+        return  # the scripted decode saw a token it did not select
+    assert result != ((5, 6, 2), (5, 6), "eos")

@@ -153,6 +153,56 @@ def test_cancellation_and_validation():
         GenerationRequest(RequestId("x"), (), 5)
 
 
+def test_token_ids_past_the_vocabulary_are_rejected_on_the_host():
+    """An id at or above the embedding's row count never reaches the GPU: submit refuses
+    it, with the vocabulary taken from the weights or given explicitly."""
+    model = ScriptedModel()
+    allocator = cpu_allocator(torch.zeros((22, 2, 32, 16, 4, 64), dtype=torch.float16))
+
+    class Weights:
+        embedding = torch.zeros(VOCAB, 8)
+
+    worker = DecodeWorker(Weights(), allocator, prefill=model.prefill, decode=model.decode)
+    with pytest.raises(ValueError, match="vocabulary size 40"):
+        worker.submit(GenerationRequest(RequestId("big"), (1, VOCAB), 3))
+    assert worker.idle
+    worker.submit(GenerationRequest(RequestId("ok"), (1, VOCAB - 1), 3))
+    explicit = DecodeWorker(None, allocator, vocab_size=7, prefill=model.prefill, decode=model.decode)
+    with pytest.raises(ValueError, match="vocabulary size 7"):
+        explicit.submit(GenerationRequest(RequestId("big"), (7,), 3))
+    with pytest.raises(ValueError, match="vocab_size"):
+        DecodeWorker(None, allocator, vocab_size=0)
+
+
+def test_failed_prefill_releases_the_request_and_later_steps_continue():
+    """A prefill that raises during admission drops the request from the active set and
+    returns its credits; the error reaches the caller, and the next iterations admit and
+    decode the requests behind it."""
+    model = ScriptedModel()
+    worker, allocator = _worker(model, max_active=2)
+    requests = [_request("ok0", new=3), _request("bad", new=3), _request("ok1", new=3)]
+    _submit(worker, model, requests)
+    original = model.prefill
+
+    def failing(ids, weights, alloc, rid):
+        if rid == "bad":
+            original(ids, weights, alloc, rid)  # publishes its prompt, then fails
+            raise RuntimeError("injected prefill failure")
+        return original(ids, weights, alloc, rid)
+
+    worker._prefill = failing
+    worker.step()
+    with pytest.raises(RuntimeError, match="injected prefill failure"):
+        worker.step()
+    assert worker.active_ids == ("ok0",)
+    counts = allocator.capacity()
+    assert counts.active_slots == 1 and counts.reserved_blocks == requests[0].block_credits
+    results = worker.run(max_steps=10)
+    assert set(results) == {"ok0", "ok1"}
+    assert all(r.finish_reason is FinishReason.LENGTH and len(r.greedy_ids) == 3 for r in results.values())
+    assert allocator.capacity().owned_blocks == 0
+
+
 def test_decode_steps_replay_the_smallest_graph_that_holds_the_batch(monkeypatch):
     """With graph sizes (4, 2) a step of n requests replays the graph of the smallest size
     >= n, captured once on first use; a step larger than every size runs decode_paged."""
