@@ -35,15 +35,20 @@ def _say(*parts) -> None:
     sys.stdout.flush()
 
 
-def assert_max_abs(got, expected, what: str = "", atol: float = ATOL) -> float:
-    """max |got - expected| <= atol (elementwise, in float64, no relative term); both must
-    be finite. Returns the error."""
+def assert_max_abs(got, expected, what: str = "", atol: float = ATOL, rtol: float = 0.0) -> float:
+    """max |got - expected| <= atol (elementwise, in float64); both must be finite. Returns
+    the error. rtol > 0 is only for the reference's own cases with a bound tighter than
+    2e-3 (atol + rtol * |expected| there, as its assert_close), and the 2e-3 max-abs bound
+    holds as well."""
     got64 = got.detach().cpu().double()
     expected64 = expected.detach().cpu().double().reshape(got64.shape)
     assert torch.isfinite(got64).all(), f"{what}: non-finite output"
     assert torch.isfinite(expected64).all(), f"{what}: non-finite expectation"
-    error = (got64 - expected64).abs().max().item() if got64.numel() else 0.0
-    assert error <= atol, f"{what}: max |got - expected| = {error:.3e} > {atol:.1e}"
+    difference = (got64 - expected64).abs()
+    error = difference.max().item() if got64.numel() else 0.0
+    assert error <= ATOL, f"{what}: max |got - expected| = {error:.3e} > {ATOL:.1e}"
+    excess = (difference - (atol + rtol * expected64.abs())).max().item() if got64.numel() else 0.0
+    assert excess <= 0, f"{what}: max |got - expected| = {error:.3e} exceeds atol {atol:.1e} + rtol {rtol:.1e} * |expected|"
     return error
 
 
@@ -78,7 +83,7 @@ def _fp64(query, key, value):
     return ref.dense_attention_fp64(query, key, value).reshape(1, 32, 1, 64)
 
 
-def _check(query, key, value, *, layer, atol=2e-3, exact=None):
+def _check(query, key, value, *, layer, atol=ATOL, rtol=0.0, exact=None):
     """The reference GPU harness (tests/gpu/test_attention_cuda.py:93-145) on the HIP path:
     a NaN-poisoned pool with a retained sentinel request between released ones, so the
     request's table is fragmented; checks FP64 and oracle agreement, autocast invariance,
@@ -115,8 +120,8 @@ def _check(query, key, value, *, layer, atol=2e-3, exact=None):
     expected = _fp64(query.detach().cpu(), key[layer].cpu(), value[layer].cpu())
     oracle = ref.reference_paged_attention(query.detach().cpu(), pool.cpu(), layer, list(table), tokens)
     worst = Worst(f"{tokens} tokens, layer {layer}")
-    worst.oracle = assert_max_abs(actual, oracle, "vs oracle", atol)
-    worst.fp64 = assert_max_abs(actual, expected, "vs fp64", atol)
+    worst.oracle = assert_max_abs(actual, oracle, "vs oracle", atol, rtol)
+    worst.fp64 = assert_max_abs(actual, expected, "vs fp64", atol, rtol)
     worst.report()
     if exact is not None:
         assert torch.equal(actual.cpu(), torch.full_like(actual.cpu(), exact) if not callable(exact) else exact())
@@ -157,7 +162,9 @@ def test_tiny_probabilities_survive_until_value_accumulation(device):
     value[:, 0] = 0
     query = torch.zeros(1, 32, 1, 64, dtype=torch.float16, device=device)
     query[..., 0] = 1
-    out = _check(query, key, value, layer=0, atol=1e-6)
+    # tests/unit/test_attention.py:224-242 bounds this case by atol=1e-6, rtol=2e-3 (the
+    # output is about 2.2e-3, where one fp16 ulp is 1.9e-6)
+    out = _check(query, key, value, layer=0, atol=1e-6, rtol=2e-3)
     assert (out > 0).all()
 
 

@@ -680,8 +680,9 @@ def test_worker_streams_equal_each_request_generated_alone(device, graph_batch, 
 @pytest.mark.parametrize("use_graph", [False, True])
 def test_decode_at_the_last_context_position(device, use_graph):
     """tests/unit/test_decoder.py:359-378: 2047 cached positions; decode writes position 2047
-    (block 127, slot 15) and the logits match the contiguous fp32 decode; the next decode
-    is refused with ValueError and changes nothing (counts, length, pool bytes)."""
+    (block 127, slot 15) and the logits match the contiguous fp32 decode (new K/V: layer 0
+    within 2e-3, every layer as accurate as the CPU fp16 forward against fp32); the next
+    decode is refused with ValueError and changes nothing (counts, length, pool bytes)."""
     weights = _synthetic(device)
     host_weights = _cpu(weights)
     pool = torch.zeros(22, 2, 128, 16, 4, 64, dtype=torch.float16, device=device)
@@ -699,13 +700,19 @@ def test_decode_at_the_last_context_position(device, use_graph):
     assert logits.shape == (1, 1, 31) and torch.isfinite(logits).all()
     assert allocator.cached_length(request) == 2048
     expected, new_cache = dref.decode_fp32(torch.tensor([[3]]), cache, host_weights)
+    _, exact_cache = dref.forward(
+        torch.tensor([[3]]), _fp32(host_weights), [(k.float(), v.float()) for k, v in cache], fp32_attention=True
+    )
     torch.testing.assert_close(logits.cpu(), expected, atol=5e-3, rtol=5e-3)
     block = allocator.block_table(request)[127]
     got = _pool_cache(allocator, request)
     for layer in range(22):
         for kind in range(2):
             assert torch.equal(got[layer][kind][:, :, :2047], cache[layer][kind])
-            torch.testing.assert_close(got[layer][kind][:, :, 2047], new_cache[layer][kind][:, :, 2047], atol=2e-3, rtol=0)
+            new = got[layer][kind][:, :, 2047]
+            if layer == 0:  # no upstream GEMM or attention noise: the reference's 2e-3
+                torch.testing.assert_close(new, new_cache[0][kind][:, :, 2047], atol=2e-3, rtol=0)
+            _as_accurate(new, new_cache[layer][kind][:, :, 2047], exact_cache[layer][kind][:, :, 2047])
     assert torch.isfinite(pool[:, :, block, 15]).all()
     counts = allocator.capacity()
     before = pool.clone()
@@ -778,9 +785,10 @@ def test_decode_step_b128_at_the_bench_workload(device):
     One DecodeGraph step, then one eager decode_paged step. For ten rows per step (the
     shortest and longest, a row whose new token opens a fresh block, one filling the last
     slot of a block, and random rows) the logits are as close to an fp32 evaluation as the
-    CPU fp16 forward is (started from the GPU's own cache), layer 0's new K/V is within
-    2e-3 of the oracle, and the greedy token agrees wherever the fp32 top-2 margin exceeds
-    that noise. Every row: finite logits, one more cached position, old slots unchanged."""
+    CPU fp16 forward is (started from the GPU's own cache; error model below), layer 0's
+    new K/V is within 2e-3 of the oracle, and the greedy token agrees wherever the fp32
+    top-2 margin exceeds that noise. Every row: finite logits, one more cached position,
+    old slots unchanged."""
     from tests.support import fragmented_decode_cache
 
     batch = 128
@@ -797,7 +805,7 @@ def test_decode_step_b128_at_the_bench_workload(device):
     graph = dec.DecodeGraph(weights, allocator, batch)
     checked = [0, 1, 2, 3] + [int(b) for b in rng.choice(np.arange(4, batch), size=6, replace=False)]
     tokens = torch.from_numpy(rng.integers(0, 32000, size=(batch, 1))).to(device)
-    agreements = 0
+    errors, kv_gaps, argmax = [], [], []
     for name, step in (("graph", graph.step), ("eager", lambda ids, rids: dec.decode_paged(ids, weights, allocator, rids))):
         old_lengths = [allocator.cached_length(r) for r in requests]
         caches = {b: _pool_cache(allocator, requests[b]) for b in checked}
@@ -818,19 +826,39 @@ def test_decode_step_b128_at_the_bench_workload(device):
             fp32 = dref.forward(
                 tokens[b : b + 1].cpu(), exact, [(k.float(), v.float()) for k, v in caches[b]], fp32_attention=True
             )[0]
-            _as_accurate(logits[b : b + 1], cpu16, fp32)
+            gpu_err = (logits[b : b + 1].float().cpu() - fp32.float()).abs()
+            cpu_err = (cpu16.float() - fp32.float()).abs()
+            errors.append(
+                (name, b, float(gpu_err.max()), float(cpu_err.max()), float(gpu_err.pow(2).mean().sqrt()),
+                 float(cpu_err.pow(2).mean().sqrt()))
+            )
+            print(
+                f"  {name} row {b} len {old_lengths[b]}: max |gpu - fp32| {errors[-1][2]:.4f} |cpu16 - fp32| "
+                f"{errors[-1][3]:.4f}  rms {errors[-1][4]:.5f} / {errors[-1][5]:.5f}",
+                flush=True,
+            )
             got = _pool_cache(allocator, request)
             for kind in range(2):
-                torch.testing.assert_close(
-                    got[0][kind][:, :, old_lengths[b]], new_cache[0][kind][:, :, old_lengths[b]], atol=2e-3, rtol=0
-                )
+                kv_gaps.append(_gap(got[0][kind][:, :, old_lengths[b]], new_cache[0][kind][:, :, old_lengths[b]]))
             top = fp32.flatten().topk(2).values
             if float(top[0] - top[1]) > 4 * _gap(cpu16, fp32):
-                assert int(logits[b].argmax()) == int(fp32.argmax()), (name, b)
-                agreements += 1
+                argmax.append((name, b, int(logits[b].argmax()), int(fp32.argmax())))
         print(f"decode step b128 ({name}): {len(checked)} rows checked against the oracle", flush=True)
         tokens = logits.argmax(-1)
-    assert agreements >= 4  # the argmax condition is not vacuous
+    print(f"  layer-0 new K/V: max |gpu - oracle| {max(kv_gaps):.2e}", flush=True)
+    # Error model at this size: the GPU and the CPU fp16 forwards both round 22 layers of
+    # fp16 GEMM outputs, so their errors against fp32 have the same distribution; each row's
+    # RMS over the 32000 logits is a stable statistic of it, while one row's maximum is an
+    # extreme value that scatters by tens of percent between two equally accurate
+    # computations. So: every row's RMS error within 1.25x the CPU's, and every row's
+    # maximum within 1.25x the largest CPU maximum over the checked rows, plus 2e-3.
+    cpu_worst = max(e[3] for e in errors)
+    for name, b, gpu_max, _, gpu_rms, cpu_rms in errors:
+        assert gpu_rms <= 1.25 * cpu_rms, (name, b, gpu_rms, cpu_rms)
+        assert gpu_max <= 1.25 * cpu_worst + 2e-3, (name, b, gpu_max, cpu_worst)
+    assert max(kv_gaps) <= 2e-3
+    assert all(got == want for _, _, got, want in argmax), argmax
+    assert len(argmax) >= 4  # the argmax condition is not vacuous
 
 
 def _worker_stream_matches_generate(request, result, host_weights, tie: float = 1e-2) -> int:
