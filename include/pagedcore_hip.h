@@ -95,6 +95,27 @@ int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t
 int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks);
 
 /*
+ * pc_paged_decode_attn without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It has no counterpart in the reference, which allocates its score buffer
+ * per call (src/pagedcore/attention.py:36).
+ *
+ * The split-K partials go to a device array inside the library, one per GPU, of
+ * PC_ATTN_NOALLOC_SCRATCH_BYTES bytes, held until the process ends; its address is looked
+ * up once per device (hipGetSymbolAddress) on the first call there. The call allocates and
+ * frees nothing. Shapes whose workspace (pc_attn_workspace_bytes) exceeds the array are
+ * refused with PC_ERR_ARGUMENT before any HIP call (32 MiB covers, e.g., batch 256 with
+ * 128-block tables). `stream` must belong to the current device. Every call on one GPU
+ * shares that GPU's array: calls that overlap in time on one GPU (concurrent streams,
+ * threads) race and give wrong rows; calls ordered on one stream are safe. Arguments and
+ * results are otherwise those of pc_paged_decode_attn.
+ */
+#define PC_ATTN_NOALLOC_SCRATCH_BYTES (32LL << 20)
+int pc_paged_decode_attn_noalloc(void* out, const void* query, const void* pool, int64_t num_blocks, int32_t layer,
+                                 const int32_t* context_lens, int32_t batch, int32_t max_blocks, const int32_t* plan,
+                                 int32_t num_records, void* stream);
+
+/*
  * Host-side decode plan (no device access). context_lens [batch] and block_tables
  * [batch][max_blocks] are HOST arrays (row b: sequence b's physical blocks in logical order,
  * only the first ceil(len / 16) read); plan is HOST memory of `capacity` records. Writes one

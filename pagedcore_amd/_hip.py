@@ -47,6 +47,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pc_kv_append.argtypes = [_p, _i64, _i32, _i32, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _p]
     lib.pc_paged_decode_attn.restype = ctypes.c_int
     lib.pc_paged_decode_attn.argtypes = [_p, _p, _p, _i64, _i32, _p, _i32, _i32, _p, _i32, _p, _p]
+    lib.pc_paged_decode_attn_noalloc.restype = ctypes.c_int
+    lib.pc_paged_decode_attn_noalloc.argtypes = [_p, _p, _p, _i64, _i32, _p, _i32, _i32, _p, _i32, _p]
     lib.pc_attn_plan.restype = _i32
     lib.pc_attn_plan.argtypes = [_p, _p, _i32, _i32, _p, _i64]
     lib.pc_attn_plan_record_ints.restype = _i32

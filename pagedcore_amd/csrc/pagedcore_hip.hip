@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include <math.h>
@@ -593,6 +594,34 @@ int check_attn_shape(int32_t batch, int32_t max_blocks) {
   return PC_OK;
 }
 
+// Split-K scratch of pc_paged_decode_attn_noalloc: a file-scope device array, one copy per
+// GPU, held until the process ends. Host code never passes `scratch` itself to a kernel (in
+// host code the name is a stand-in, not a device address); it uses the address
+// hipGetSymbolAddress returns for the device, looked up once per device.
+constexpr int64_t kNoAllocScratchBytes = PC_ATTN_NOALLOC_SCRATCH_BYTES;
+static_assert(kNoAllocScratchBytes % 256 == 0, "the scratch keeps the workspace's 256-byte alignment");
+__device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `device` (which must be current), or null with the error
+// recorded.
+void* scratch_address(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr) {
+      set_error(PC_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", device, hipGetErrorString(err));
+      return nullptr;
+    }
+    g_scratch_ptr[device] = ptr;
+  }
+  return g_scratch_ptr[device];
+}
+
 }  // namespace
 
 extern "C" {
@@ -763,6 +792,33 @@ int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t
     return check_launch("paged_decode_merge");
   }
   return PC_OK;
+}
+
+int pc_paged_decode_attn_noalloc(void* out, const void* query, const void* pool, int64_t num_blocks, int32_t layer,
+                                 const int32_t* context_lens, int32_t batch, int32_t max_blocks, const int32_t* plan,
+                                 int32_t num_records, void* stream) {
+  // The size check comes first: a call beyond the scratch is refused before any HIP call.
+  if (int rc = check_attn_shape(batch, max_blocks)) return rc;
+  const int64_t need = static_cast<int64_t>(batch) * kKVHeads * items_per_sequence(max_blocks) * kPartFloats * 4;
+  if (need > kNoAllocScratchBytes) {
+    return set_error(PC_ERR_ARGUMENT,
+                     "batch %d with %d-block tables needs %lld bytes of split-K scratch; the allocation-free entry "
+                     "point holds %lld (use pc_paged_decode_attn with a workspace)",
+                     batch, max_blocks, static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int device = -1, current = -1;
+  if (hipStreamGetDevice(s, &device) != hipSuccess || hipGetDevice(&current) != hipSuccess) {
+    return set_error(PC_ERR_LAUNCH, "cannot determine the stream's device");
+  }
+  if (device != current) {
+    return set_error(PC_ERR_ARGUMENT, "stream is on device %d but device %d is current", device, current);
+  }
+  if (device < 0 || device >= kMaxDevices) return set_error(PC_ERR_ARGUMENT, "device %d out of range", device);
+  void* workspace = scratch_address(device);
+  if (!workspace) return PC_ERR_LAUNCH;
+  return pc_paged_decode_attn(out, query, pool, num_blocks, layer, context_lens, batch, max_blocks, plan, num_records,
+                              workspace, stream);
 }
 
 }  // extern "C"

@@ -196,3 +196,14 @@ def test_gpu_pool_allocator_requires_the_library(monkeypatch, tmp_path):
     with pytest.raises(RuntimeError, match="KV writes run on the GPU"):
         allocator.append(RequestId("a"), *[torch.zeros(22, 1, 4, 64, dtype=torch.float16)] * 2)
     assert allocator.cached_length(RequestId("a")) == 0
+
+
+def test_noalloc_attention_refuses_oversize_shapes_before_any_hip_call():
+    """The allocation-free entry point checks the shape against its 32 MiB device array
+    first, so the refusal needs no GPU (nothing else is touched)."""
+    lib = _hip.load()
+    assert lib.pc_attn_workspace_bytes(512, 128) > 32 << 20
+    status = lib.pc_paged_decode_attn_noalloc(None, None, None, 8, 0, None, 512, 128, None, 1, None)
+    assert status == 1 and b"allocation-free entry point holds" in lib.pc_last_error()
+    assert lib.pc_paged_decode_attn_noalloc(None, None, None, 8, 0, None, 1, 0, None, 1, None) == 1
+    assert b"max_blocks" in lib.pc_last_error()
