@@ -325,7 +325,32 @@ def cpu_append_baseline(w: workloads.PromptAppend, table: Sequence[int], seconds
     }
 
 
-def run_single_decode(calls: int = 200) -> dict:
+def cpu_single_decode_baseline(pool: Tensor, query: Tensor, table: Sequence[int], seconds: float) -> dict:
+    """Latency of the oracle's port of the reference's paged_attention (attention.py:14-53)
+    on the single-sequence case, on this host's cores: one call per iteration, repeated for
+    about `seconds` after one untimed call (copying the pool to host memory is not timed)."""
+    from oracle import paged_reference as ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    host_pool, host_query = pool.cpu(), query.reshape(1, 32, 1, 64).cpu()
+    ref.reference_paged_attention(host_query, host_pool, 0, list(table), 128)
+    done, elapsed = 0, 0.0
+    while elapsed < seconds:
+        start = time.perf_counter()
+        ref.reference_paged_attention(host_query, host_pool, 0, list(table), 128)
+        elapsed += time.perf_counter() - start
+        done += 1
+    return {
+        "value": round(elapsed / done * 1e6, 2),
+        "unit": "us per call",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{done} calls on the same 128-token sequence, {elapsed:.1f} s on {cores} threads",
+    }
+
+
+def run_single_decode(calls: int = 200, cpu_seconds: float = 0.0) -> dict:
     """The single-sequence decode case: one query [1, 32, 64] over 128 cached tokens (8
     blocks of a random table in a NaN-poisoned 64-block pool), one layer. Latency-bound
     (139 KB of K/V, Q and O), so it is reported as the average duration of one
@@ -366,12 +391,15 @@ def run_single_decode(calls: int = 200) -> dict:
     total_ms = _timed(graph.replay, 1, device)
     nbytes = attention_bytes(lengths)
     us = total_ms / calls * 1e3
-    return {
+    result = {
         "workload": "one sequence, 128 cached tokens on a random 8-block table of a 64-block pool, one layer",
         "us_per_call": round(us, 3),
         "bytes_per_call": int(nbytes),
         "gbps": round(nbytes / (us / 1e6) / 1e9, 2),
     }
+    if cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_single_decode_baseline(pool, query, table.tolist(), cpu_seconds)
+    return result
 
 
 def run_prompt_append(steps: int, cpu_seconds: float = 0.0) -> dict:
@@ -631,14 +659,85 @@ def cpu_baseline(layers: DecodeLayers, seconds: float) -> dict:
     }
 
 
+def cpu_bookkeeping_baseline(layers: DecodeLayers, seconds: float) -> dict:
+    """The secondary CPU number: the reference's per-row decode work including its
+    allocator bookkeeping, on the same workload. Per sequence and layer, as its decode loop
+    runs it (decoder.py:180-194): write_decode_layer (kv_cache.py:221-246: one
+    _assert_accounting, then the new token's K/V copies) and paged_attention
+    (attention.py:14-53, whose two iter_layer_blocks traversals each run _assert_accounting,
+    kv_cache.py:248-270). _assert_accounting is the oracle's restatement of
+    kv_cache.py:314-357 over this workload's state: 64 requests holding their tables in the
+    8192-block pool, the rest free. Sequences are taken in order, cycling the layers, for
+    about `seconds`; the step figure scales the mean per-sequence time to 64 x 22."""
+    from oracle import paged_reference as ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    w = layers.w
+    tables = [tuple(int(x) for x in w.tables[b, : (int(w.lengths[b]) + 15) // 16]) for b in range(w.batch)]
+    sequences = {f"seq{b}": ref.SequenceRecord(f"seq{b}", 128, int(w.lengths[b]), tables[b]) for b in range(w.batch)}
+    owners = {block: f"seq{b}" for b in range(w.batch) for block in tables[b]}
+    free = [block for block in range(w.num_blocks - 1, -1, -1) if block not in owners]
+    assert ref.reference_assert_accounting(sequences, free, owners, w.num_blocks)[2] == len(owners)
+    gen = torch.Generator().manual_seed(3)
+    done, elapsed, row = 0, 0.0, 0
+    while elapsed < seconds:
+        layer, b = divmod(row, w.batch)
+        layer %= LAYERS
+        length = int(w.lengths[b])
+        index = torch.tensor(tables[b], dtype=torch.long, device=layers.device)
+        sub = torch.empty((LAYERS, 2, len(tables[b]), 16, 4, 64), dtype=torch.float16)
+        sub[layer] = layers.pool[layer].index_select(1, index).cpu()
+        host = sub.view(torch.int16).numpy().view(np.uint16)
+        new_kv = torch.randn((2, 4, 64), generator=gen).half().view(torch.int16).numpy().view(np.uint16)
+        query = layers.queries[layer, b].reshape(1, 32, 1, 64).cpu()
+        local = list(range(len(tables[b])))
+        start = time.perf_counter()
+        ref.reference_assert_accounting(sequences, free, owners, w.num_blocks)  # write_decode_layer
+        ref.reference_write_decode(host, layer, local, length, new_kv[0], new_kv[1])
+        ref.reference_assert_accounting(sequences, free, owners, w.num_blocks)  # first traversal
+        ref.reference_assert_accounting(sequences, free, owners, w.num_blocks)  # second traversal
+        ref.reference_paged_attention(query, sub, layer, local, length)
+        elapsed += time.perf_counter() - start
+        done += 1
+        row += 1
+    per_row = elapsed / done
+    step_s = per_row * w.batch * LAYERS
+    return {
+        "value": round(attention_bytes(w.lengths) * LAYERS / step_s / 1e9, 4),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{done} sequence-layers of the same workload, each: write_decode_layer's accounting check and "
+        f"K/V copies, then paged_attention with its two accounting checks, {elapsed:.1f} s on {cores} threads, "
+        f"{per_row * 1e3:.2f} ms per sequence-layer; scaled to {w.batch} sequences x 22 layers: {step_s:.2f} s per "
+        f"step, {w.batch / step_s:.2f} decode tokens/s (GB/s over the attention's algorithmic bytes)",
+    }
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_decode_attention_b64_hbm_traffic.txt")
 EXTRA_CPU_SECONDS = 3.0  # CPU baseline sample of each extra workload that has one
 
 
+def kernel_source_hash() -> str:
+    """sha256 (first 16 hex digits) of the library's kernel sources, csrc/*.hip and *.h in
+    name order: the key under which a counter summary is valid."""
+    import hashlib
+
+    folder = os.path.join(ROOT, "pagedcore_amd", "csrc")
+    digest = hashlib.sha256()
+    for name in sorted(os.listdir(folder)):
+        if name.endswith((".hip", ".h")):
+            with open(os.path.join(folder, name), "rb") as handle:
+                digest.update(name.encode() + b"\0" + handle.read())
+    return digest.hexdigest()[:16]
+
+
 def measured_traffic() -> int | None:
-    """HBM bytes per attention call (item + merge kernels) from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary, scaled by the plain-copy calibration recorded there;
-    None unless that summary was made for this library version."""
+    """HBM bytes per attention call from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary, scaled by the plain-copy calibration recorded there; None unless that summary
+    was made from exactly these kernel sources (its source_sha256 equals
+    kernel_source_hash())."""
     try:
         with open(TRAFFIC_FILE) as handle:
             fields = dict(
@@ -648,7 +747,7 @@ def measured_traffic() -> int | None:
         return None
     fields = {k.strip(): v.strip() for k, v in fields.items()}
     try:
-        same = int(fields["abi_version"]) == _hip.ABI_VERSION
+        same = fields["source_sha256"] == kernel_source_hash()
         return int(fields["traffic_bytes_per_call"]) if same else None
     except (KeyError, ValueError):
         return None
@@ -671,7 +770,7 @@ def run_extra(selected: set, steps: int, cpu_seconds: float = 0.0) -> dict:
     baseline of about `cpu_seconds` where the workload has one; 0 = none)."""
     extra = {}
     if "single_decode" in selected:
-        extra["single_decode_c1"] = run_single_decode()
+        extra["single_decode_c1"] = run_single_decode(cpu_seconds=cpu_seconds)
         print(f"single decode: {extra['single_decode_c1']}", file=sys.stderr, flush=True)
     if "prompt_append" in selected:
         extra["prompt_append"] = run_prompt_append(max(10, steps), cpu_seconds)
@@ -748,6 +847,8 @@ def main() -> int:
     baseline = None
     if not args.no_cpu_baseline:
         baseline = cpu_baseline(layers, args.cpu_seconds)
+        baseline["with_allocator_bookkeeping"] = cpu_bookkeeping_baseline(layers, EXTRA_CPU_SECONDS)
+        print(f"cpu baseline: {baseline}", file=sys.stderr, flush=True)
     del layers, r["layers"]
     torch.cuda.empty_cache()
     extra = run_extra(selected, args.steps, 0.0 if args.no_cpu_baseline else EXTRA_CPU_SECONDS)
@@ -778,7 +879,7 @@ def main() -> int:
             "launch": "hip_graph" if r["graph"] else "eager",
         },
         "hbm_fraction": round(r["gbps"] / PEAK_HBM_GBPS, 4),
-        "decode_tokens_per_s": round(r["tokens_per_s"], 1),
+        "attention_only_decode_tokens_per_s": round(r["tokens_per_s"], 1),
         "step_ms_median": round(r["step_ms_median"], 4),
         "step_ms_min": round(r["step_ms_min"], 4),
         "step_ms_max": round(r["step_ms_max"], 4),

@@ -151,6 +151,65 @@ def f16_bits(tensor: Tensor) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------------------
+# Allocator bookkeeping
+# ---------------------------------------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class SequenceRecord:
+    """One request's bookkeeping as the reference allocator keeps it: its reservation's
+    request id and block credits, its cached length and its block table."""
+
+    request_id: str
+    credits: int
+    length: int
+    blocks: tuple
+
+
+def reference_assert_accounting(
+    sequences: Dict[str, SequenceRecord], free_blocks: List[int], block_owners: Dict[int, str], total_blocks: int
+) -> Tuple[int, int, int, int, int, int]:
+    """KVAllocator._assert_accounting (kv_cache.py:314-357), check for check and in the same
+    order, with the same messages; returns CapacityCounts' fields (total, free, owned,
+    reserved, active slots, live cached token slots). O(pool blocks) per call: it builds the
+    full set of block ids each time, which is the reference's per-call host cost."""
+    for request_id, sequence in sequences.items():
+        if (
+            sequence.request_id != request_id
+            or type(sequence.length) is not int
+            or not 0 <= sequence.length <= 2048
+            or type(sequence.blocks) is not tuple
+            or len(sequence.blocks) != (sequence.length + 15) // 16
+            or not len(sequence.blocks) <= sequence.credits <= 128
+        ):
+            raise RuntimeError("corrupt KV block table or reservation")
+    assigned = [block for sequence in sequences.values() for block in sequence.blocks]
+    if any(type(block) is not int or not 0 <= block < total_blocks for block in free_blocks + assigned):
+        raise RuntimeError("invalid physical KV block")
+    owned = set(assigned)
+    free = set(free_blocks)
+    if len(assigned) != len(owned):
+        raise RuntimeError("physical KV blocks must have unique owners")
+    if len(free_blocks) != len(free):
+        raise RuntimeError("free KV blocks must be unique")
+    if not free.isdisjoint(owned):
+        raise RuntimeError("owned KV blocks must not be free")
+    if free | owned != set(range(total_blocks)):
+        raise RuntimeError("KV blocks must cover the pool")
+    owners = {block: request_id for request_id, sequence in sequences.items() for block in sequence.blocks}
+    if owners != block_owners:
+        raise RuntimeError("KV blocks are not owned by the recorded requests")
+    return (
+        total_blocks,
+        len(free_blocks),
+        len(assigned),
+        sum(sequence.credits for sequence in sequences.values()),
+        len(sequences),
+        sum(sequence.length for sequence in sequences.values()),
+    )
+
+
+# ---------------------------------------------------------------------------------------
 # Block choice
 # ---------------------------------------------------------------------------------------
 

@@ -346,3 +346,132 @@ def test_planted_write_decode_off_by_one_is_caught(shift):
             block, slot = blocks[(length - 1) // 16], (length - 1) % 16
             base = (((layer * 2) * num_blocks + block) * 16 + slot) * 256
             assert np.array_equal(pool.reshape(-1)[base : base + 256], key.reshape(-1))
+
+
+# --- Allocator bookkeeping (kv_cache.py:314-357) ----------------------------------------------
+
+
+class _Model:
+    """Bookkeeping driven through the restated LIFO rules, checked by the restated
+    _assert_accounting after each step."""
+
+    def __init__(self, total):
+        self.total = total
+        self.lifo = ref.LifoFreeList.fresh(total)
+        self.sequences, self.owners = {}, {}
+
+    def create(self, rid, credits):
+        self.sequences[rid] = ref.SequenceRecord(rid, credits, 0, ())
+
+    def append(self, rid, tokens):
+        old = self.sequences[rid]
+        new = self.lifo.grow_to(rid, old.length + tokens)
+        for block in new:
+            self.owners[block] = rid
+        self.sequences[rid] = ref.SequenceRecord(rid, old.credits, old.length + tokens, old.blocks + tuple(new))
+
+    def release(self, rid):
+        for block in self.sequences.pop(rid).blocks:
+            del self.owners[block]
+        self.lifo.release(rid)
+
+    def counts(self):
+        return ref.reference_assert_accounting(self.sequences, self.lifo.free, self.owners, self.total)
+
+
+def test_accounting_reproduces_the_reference_counts():
+    # tests/unit/test_kv_cache.py:453-483
+    m = _Model(8)
+    assert m.counts() == (8, 8, 0, 0, 0, 0)
+    m.create("a", 3)
+    assert m.counts() == (8, 8, 0, 3, 1, 0)
+    m.create("b", 2)
+    assert m.counts() == (8, 8, 0, 5, 2, 0)
+    for rid, tokens, expected in (
+        ("a", 15, (8, 7, 1, 5, 2, 15)),
+        ("b", 16, (8, 6, 2, 5, 2, 31)),
+        ("a", 1, (8, 6, 2, 5, 2, 32)),
+        ("a", 1, (8, 5, 3, 5, 2, 33)),
+        ("a", 16, (8, 4, 4, 5, 2, 49)),
+    ):
+        m.append(rid, tokens)
+        assert m.counts() == expected
+    m.release("a")
+    assert m.counts() == (8, 7, 1, 2, 1, 16)
+    m.release("b")
+    assert m.counts() == (8, 8, 0, 0, 0, 0)
+    # tests/unit/test_kv_cache.py:344-382: a staged decode step that borrows one block for
+    # each of two 16-token requests leaves the pool fully owned, 34 live slots
+    m = _Model(4)
+    for rid in ("first", "second"):
+        m.create(rid, 2)
+        m.append(rid, 16)
+    tables = m.lifo.decode_step({"first": 16, "second": 16})
+    for rid in ("first", "second"):
+        m.sequences[rid] = ref.SequenceRecord(rid, 2, 17, tuple(tables[rid]))
+        for block in tables[rid]:
+            m.owners[block] = rid
+    assert m.counts() == (4, 0, 4, 4, 2, 34)
+
+
+def _corrupted(kind):
+    m = _Model(6)
+    m.create("a", 3)
+    m.append("a", 17)
+    m.create("b", 1)
+    m.append("b", 5)
+    a = m.sequences["a"]
+    if kind == "table":
+        m.sequences["a"] = ref.SequenceRecord("a", 3, 40, a.blocks)  # 40 tokens need 3 blocks
+    elif kind == "credits":
+        m.sequences["a"] = ref.SequenceRecord("a", 1, 17, a.blocks)
+    elif kind == "invalid":
+        m.lifo.free[0] = 6
+    elif kind == "shared":
+        m.sequences["b"] = ref.SequenceRecord("b", 1, 5, (a.blocks[0],))
+    elif kind == "duplicate_free":
+        m.lifo.free.append(m.lifo.free[0])
+    elif kind == "owned_free":
+        m.lifo.free.append(a.blocks[1])
+        m.lifo.free.remove(m.lifo.free[0])
+    elif kind == "missing":
+        m.lifo.free.pop()
+    elif kind == "owner":
+        m.owners[a.blocks[0]] = "b"
+    return m
+
+
+@pytest.mark.parametrize(
+    "kind,message",
+    [
+        ("table", "corrupt KV block table or reservation"),
+        ("credits", "corrupt KV block table or reservation"),
+        ("invalid", "invalid physical KV block"),
+        ("shared", "physical KV blocks must have unique owners"),
+        ("duplicate_free", "free KV blocks must be unique"),
+        ("owned_free", "owned KV blocks must not be free"),
+        ("missing", "KV blocks must cover the pool"),
+        ("owner", "KV blocks are not owned by the recorded requests"),
+    ],
+)
+def test_accounting_raises_the_reference_message_for_each_corruption(kind, message):
+    assert _corrupted("none").counts() == (6, 3, 3, 4, 2, 22)
+    with pytest.raises(RuntimeError, match=message):
+        _corrupted(kind).counts()
+
+
+@pytest.mark.parametrize("kind", ["missing", "duplicate_free"])
+def test_planted_accounting_mistake_is_caught(monkeypatch, kind):
+    """An accounting check that derives the free set from the owned blocks instead of
+    reading the free list returns counts for a lost or duplicated free block; the
+    corruption cases above tell the two apart."""
+    original = ref.reference_assert_accounting
+
+    def blind_to_free_list(sequences, free_blocks, block_owners, total_blocks):
+        owned = {b for s in sequences.values() for b in s.blocks}
+        return original(sequences, [b for b in range(total_blocks) if b not in owned], block_owners, total_blocks)
+
+    with pytest.raises(RuntimeError):
+        _corrupted(kind).counts()
+    monkeypatch.setattr(ref, "reference_assert_accounting", blind_to_free_list)
+    assert _corrupted(kind).counts()[0] == 6  # no error: the planted check misses the corruption
