@@ -198,6 +198,47 @@ int pc_add_rms_norm(void* out, void* hidden, const void* delta, const void* weig
 int pc_silu_mul(void* out, const void* gate_up, int64_t rows, int32_t width, void* stream);
 
 /*
+ * Split-K forms of the two consumers above, for the partial sums of pc_gemm_m128's partials
+ * epilogue: the fp16 input they replace is fp16(sum over s of parts[s]), added in split
+ * order, and everything after that is the same computation.
+ *
+ *   pc_rope_kv_append_parts: qkv_parts [splits][num_tokens][2560] fp32 in place of qkv.
+ *   pc_add_rms_norm_parts:   delta_parts [splits][rows][width] fp32 in place of delta;
+ *                            hidden = fp16(hidden + fp16(sum of delta_parts)).
+ * splits in [1, 64]; parts 16-byte aligned.
+ */
+int pc_rope_kv_append_parts(void* query_out, void* key_out, void* value_out, const float* qkv_parts, int32_t splits,
+                            const int64_t* positions, const void* rope_table, int32_t rope_positions, void* pool,
+                            int64_t num_blocks, int32_t layer, const int64_t* slot_mapping, int64_t num_tokens,
+                            void* stream);
+int pc_add_rms_norm_parts(void* out, void* hidden, const float* delta_parts, int32_t splits, const void* weight,
+                          int64_t rows, int32_t width, float eps, void* stream);
+
+/*
+ * Projection GEMM of the decode step at up to 128 rows: Y[i][j] = sum_l x[i][l] * w[j][l],
+ * fp16 inputs, fp32 accumulation.
+ *
+ * Replaces torch.nn.functional.linear on the decode step's activations (reference
+ * src/pagedcore/dense.py:91-104, called per layer by src/pagedcore/decoder.py:156-199) for
+ * the q|k|v, o_proj, gate|up and down projections at batch <= 128.
+ *
+ *   x    [m][k] fp16, m in [1, 128];  w [n][k] fp16 (the weight as stored, row-major)
+ *   out, by epilogue:
+ *     PC_GEMM_PARTIALS  [splits][m][n] fp32: split s sums l in [s k / splits, (s + 1) k / splits)
+ *     PC_GEMM_HALF      [m][n] fp16, fp16(Y) (splits = 1)
+ *     PC_GEMM_SWIGLU    [m][n / 2] fp16 (splits = 1), w the stacked [gate_proj | up_proj]
+ *                       weight: out[i][j] = fp16(fp16(silu(fp16(Y[i][j]))) * fp16(Y[i][n/2 + j]))
+ *                       (the rounding of pc_silu_mul applied to the fp16 projections)
+ * k / splits a multiple of 64; n a multiple of 32 (of 64 for PC_GEMM_SWIGLU); all buffers
+ * 16-byte aligned; out must not overlap x or w.
+ */
+#define PC_GEMM_PARTIALS 0
+#define PC_GEMM_HALF 1
+#define PC_GEMM_SWIGLU 2
+int pc_gemm_m128(void* out, const void* x, const void* w, int32_t m, int32_t n, int32_t k, int32_t splits,
+                 int32_t epilogue, void* stream);
+
+/*
  * Causal attention of one prompt over its contiguous K/V (the prefill of one sequence).
  *
  * Replaces the prompt's dense_attention (reference src/pagedcore/dense.py:69-81, called by

@@ -17,7 +17,7 @@ import numpy as np
 import torch
 from torch import Tensor
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 LIBRARY_NAME = "libpagedcore_hip.so"
 
 _lock = threading.Lock()
@@ -63,6 +63,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pc_silu_mul.argtypes = [_p, _p, _i64, _i32, _p]
     lib.pc_prefill_attention.restype = ctypes.c_int
     lib.pc_prefill_attention.argtypes = [_p, _p, _p, _p, _i32, _p]
+    lib.pc_rope_kv_append_parts.restype = ctypes.c_int
+    lib.pc_rope_kv_append_parts.argtypes = [_p, _p, _p, _p, _i32, _p, _p, _i32, _p, _i64, _i32, _p, _i64, _p]
+    lib.pc_add_rms_norm_parts.restype = ctypes.c_int
+    lib.pc_add_rms_norm_parts.argtypes = [_p, _p, _p, _i32, _p, _i64, _i32, ctypes.c_float, _p]
+    lib.pc_gemm_m128.restype = ctypes.c_int
+    lib.pc_gemm_m128.argtypes = [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p]
 
 
 def load() -> ctypes.CDLL:
@@ -331,6 +337,84 @@ def rope_kv_append(
         _stream(qkv.device),
     )
     _check(lib, "pc_rope_kv_append", status)
+
+
+def rope_kv_append_parts(
+    query_out: Tensor,
+    qkv_parts: Tensor,
+    positions: Tensor,
+    rope_table: Tensor,
+    *,
+    key_out: Optional[Tensor] = None,
+    value_out: Optional[Tensor] = None,
+    pool: Optional[Tensor] = None,
+    layer: int = 0,
+    slot_mapping: Optional[Tensor] = None,
+) -> None:
+    """rope_kv_append with the q | k | v row given as split-K partial sums: qkv_parts
+    contiguous fp32 [splits, tokens, 2560] (gemm_m128's partials), rounded to fp16 once."""
+    lib = load()
+    if qkv_parts.dim() != 3 or qkv_parts.dtype != torch.float32 or not qkv_parts.is_contiguous():
+        raise HipExtensionError("qkv_parts must be contiguous fp32 [splits, tokens, 2560]")
+    status = lib.pc_rope_kv_append_parts(
+        query_out.data_ptr(),
+        _ptr(key_out),
+        _ptr(value_out),
+        qkv_parts.data_ptr(),
+        qkv_parts.shape[0],
+        positions.data_ptr(),
+        rope_table.data_ptr(),
+        rope_table.shape[0],
+        _ptr(pool),
+        pool.shape[2] if pool is not None else 0,
+        layer,
+        _ptr(slot_mapping),
+        qkv_parts.shape[1],
+        _stream(qkv_parts.device),
+    )
+    _check(lib, "pc_rope_kv_append_parts", status)
+
+
+def add_rms_norm_parts(out: Tensor, hidden: Tensor, delta_parts: Tensor, weight: Tensor, eps: float = 1e-5) -> None:
+    """add_rms_norm with delta given as split-K partial sums: delta_parts contiguous fp32
+    [splits, rows, width]; hidden = fp16(hidden + fp16(sum of the splits))."""
+    lib = load()
+    if delta_parts.dim() != 3 or delta_parts.shape[1:] != hidden.shape or delta_parts.dtype != torch.float32:
+        raise HipExtensionError("delta_parts must be fp32 [splits, rows, width] matching hidden")
+    if not delta_parts.is_contiguous():
+        raise HipExtensionError("delta_parts must be contiguous")
+    status = lib.pc_add_rms_norm_parts(
+        out.data_ptr(), hidden.data_ptr(), delta_parts.data_ptr(), delta_parts.shape[0], weight.data_ptr(),
+        hidden.shape[0], hidden.shape[1], eps, _stream(hidden.device),
+    )
+    _check(lib, "pc_add_rms_norm_parts", status)
+
+
+GEMM_PARTIALS, GEMM_HALF, GEMM_SWIGLU = 0, 1, 2
+
+
+def gemm_m128(out: Tensor, x: Tensor, w: Tensor, *, splits: int = 1, epilogue: int = GEMM_PARTIALS) -> None:
+    """Decode-step projection x @ w.T for up to 128 rows of x (pc_gemm_m128): x fp16 [m, k],
+    w fp16 [n, k], both contiguous. out: fp32 [splits, m, n] (GEMM_PARTIALS), fp16 [m, n]
+    (GEMM_HALF) or fp16 [m, n // 2] (GEMM_SWIGLU, w the stacked [gate | up] weight)."""
+    lib = load()
+    m, k = x.shape
+    n = w.shape[0]
+    expected = {
+        GEMM_PARTIALS: ((splits, m, n), torch.float32),
+        GEMM_HALF: ((m, n), torch.float16),
+        GEMM_SWIGLU: ((m, n // 2), torch.float16),
+    }.get(epilogue)
+    if expected is None:
+        raise HipExtensionError(f"unknown GEMM epilogue {epilogue}")
+    if x.dtype != torch.float16 or w.dtype != torch.float16 or w.shape[1] != k:
+        raise HipExtensionError("x and w must be fp16 [m, k] and [n, k]")
+    if tuple(out.shape) != expected[0] or out.dtype != expected[1]:
+        raise HipExtensionError(f"out must be {expected[1]} {list(expected[0])}")
+    if not (x.is_contiguous() and w.is_contiguous() and out.is_contiguous()):
+        raise HipExtensionError("x, w and out must be contiguous")
+    status = lib.pc_gemm_m128(out.data_ptr(), x.data_ptr(), w.data_ptr(), m, n, k, splits, epilogue, _stream(x.device))
+    _check(lib, "pc_gemm_m128", status)
 
 
 def add_rms_norm(out: Tensor, hidden: Tensor, delta: Optional[Tensor], weight: Tensor, eps: float = 1e-5) -> None:

@@ -20,7 +20,7 @@ from typing import Dict, Iterable, List, Mapping
 HERE = os.path.dirname(os.path.abspath(__file__))
 PACKAGE = os.path.dirname(HERE)
 ROOT = os.path.dirname(PACKAGE)
-SOURCES = [os.path.join(HERE, name) for name in ("pagedcore_hip.hip", "decode_step.hip", "prefill.hip")]
+SOURCES = [os.path.join(HERE, name) for name in ("pagedcore_hip.hip", "decode_step.hip", "prefill.hip", "skinny_gemm.hip")]
 OUTPUT = os.path.join(PACKAGE, "libpagedcore_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

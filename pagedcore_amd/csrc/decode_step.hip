@@ -1,5 +1,8 @@
 // Elementwise kernels of the batched decode step around paged attention: RoPE fused with the
 // KV append, residual add fused with RMSNorm, and SiLU fused with the up-projection product.
+// The first two also take their projection input as fp32 split-K partial sums (the output of
+// pc_gemm_m128's partials epilogue), added in split order and rounded to fp16 once: the
+// value the reference's fp16 GEMM output holds, up to the order of fp32 accumulation.
 //
 // Each one reproduces the fp16 rounding points of the reference's torch expressions
 // (src/pagedcore/dense.py:17-21, 33-61, 102-104): every torch op on fp16 tensors computes
@@ -40,6 +43,26 @@ constexpr int kSiluThreads = 256;
 
 __device__ __forceinline__ _Float16 round_h(float x) { return static_cast<_Float16>(x); }
 
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+// fp16(sum over the splits of parts[s * split_stride + offset + 0..7]), added in split order.
+__device__ __forceinline__ half8_t sum_parts8(const float* parts, int64_t offset, int splits, int64_t split_stride) {
+  float4_t lo = *reinterpret_cast<const float4_t*>(parts + offset);
+  float4_t hi = *reinterpret_cast<const float4_t*>(parts + offset + 4);
+  for (int s = 1; s < splits; ++s) {
+    const float* p = parts + s * split_stride + offset;
+    lo += *reinterpret_cast<const float4_t*>(p);
+    hi += *reinterpret_cast<const float4_t*>(p + 4);
+  }
+  half8_t out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[i] = round_h(lo[i]);
+    out[i + 4] = round_h(hi[i]);
+  }
+  return out;
+}
+
 // ---------------------------------------------------------------------------------------
 // RoPE + KV append.
 //
@@ -56,12 +79,14 @@ struct RopeArgs {
   _Float16* query_out;        // [T][32][64]
   _Float16* key_out;          // [T][4][64] or null
   _Float16* value_out;        // [T][4][64] or null
-  const _Float16* qkv;        // [T][qkv_stride]: q (2048) | k (256) | v (256)
+  const _Float16* qkv;        // [T][qkv_stride]: q (2048) | k (256) | v (256); or null and
+  const float* qkv_parts;     // [splits][T][2560] fp32 partial sums of the same columns
+  int32_t splits;
   const int64_t* positions;   // [T]
   const _Float16* rope;       // [rope_positions][2][32]: cos, then sin
   _Float16* pool;             // or null
   const int64_t* slot_mapping;  // [T] or null
-  int64_t qkv_stride;
+  int64_t qkv_stride;         // qkv's row stride, or qkv_parts' split stride (T * 2560)
   int64_t slot_limit;         // num_blocks * 16
   int64_t kind_elems;         // num_blocks * 16 * 256: one (layer, kind) plane
   int32_t layer;
@@ -89,12 +114,17 @@ __device__ __forceinline__ void rotate_pair(half8_t& lo, half8_t& hi, const half
   hi = out_hi;
 }
 
+// 8 columns of token t's q | k | v row, from the fp16 row or the partial sums.
+__device__ __forceinline__ half8_t load_qkv8(const RopeArgs& a, int64_t t, int col) {
+  if (a.qkv_parts != nullptr) return sum_parts8(a.qkv_parts, t * kQkvElems + col, a.splits, a.qkv_stride);
+  return *reinterpret_cast<const half8_t*>(a.qkv + t * a.qkv_stride + col);
+}
+
 __global__ __launch_bounds__(kRopeThreads) void rope_kv_append_kernel(RopeArgs a) {
   const int64_t t = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t position = a.positions[t];
   const bool valid_position = position >= 0 && position < a.rope_positions;
-  const _Float16* row = a.qkv + t * a.qkv_stride;
   int64_t slot = -1;
   if (a.pool != nullptr && a.slot_mapping != nullptr) {
     slot = a.slot_mapping[t];
@@ -107,9 +137,9 @@ __global__ __launch_bounds__(kRopeThreads) void rope_kv_append_kernel(RopeArgs a
     const int task = is_q ? tid : tid - 128;
     const int head = task >> 2;
     const int c = task & 3;
-    const _Float16* src = row + (is_q ? 0 : kQElems) + head * kHeadDim + 8 * c;
-    half8_t lo = *reinterpret_cast<const half8_t*>(src);
-    half8_t hi = *reinterpret_cast<const half8_t*>(src + kHalfDim);
+    const int col = (is_q ? 0 : kQElems) + head * kHeadDim + 8 * c;
+    half8_t lo = load_qkv8(a, t, col);
+    half8_t hi = load_qkv8(a, t, col + kHalfDim);
     if (valid_position) {
       const _Float16* table = a.rope + position * kHeadDim + 8 * c;
       const half8_t cs = *reinterpret_cast<const half8_t*>(table);
@@ -138,7 +168,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_kv_append_kernel(RopeArgs a
     }
   } else if (tid < 176) {
     const int j = tid - 144;
-    const half8_t v = *reinterpret_cast<const half8_t*>(row + kQElems + kRowElems + 8 * j);
+    const half8_t v = load_qkv8(a, t, kQElems + kRowElems + 8 * j);
     if (a.value_out != nullptr) *reinterpret_cast<half8_t*>(a.value_out + t * kRowElems + 8 * j) = v;
     if (slot >= 0 && valid_position) *reinterpret_cast<half8_t*>(a.pool + pool_row + a.kind_elems + 8 * j) = v;
   }
@@ -159,9 +189,13 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// delta, when given, is fp16 [rows][width] or (delta_parts, splits) fp32 partial sums
+// [splits][rows][width], rounded to fp16 before the add.
 __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(_Float16* __restrict__ out,
                                                                     _Float16* __restrict__ hidden,
                                                                     const _Float16* __restrict__ delta,
+                                                                    const float* __restrict__ delta_parts,
+                                                                    int32_t splits, int64_t parts_stride,
                                                                     const _Float16* __restrict__ weight,
                                                                     int32_t width, float eps) {
 #pragma clang fp contract(off)
@@ -177,8 +211,9 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(_Float16* __
     if (chunk < chunks) {
       _Float16* p = hidden + base + 8 * chunk;
       h[k] = *reinterpret_cast<const half8_t*>(p);
-      if (delta != nullptr) {
-        const half8_t d = *reinterpret_cast<const half8_t*>(delta + base + 8 * chunk);
+      if (delta != nullptr || delta_parts != nullptr) {
+        const half8_t d = delta_parts != nullptr ? sum_parts8(delta_parts, base + 8 * chunk, splits, parts_stride)
+                                                 : *reinterpret_cast<const half8_t*>(delta + base + 8 * chunk);
 #pragma unroll
         for (int i = 0; i < 8; ++i) h[k][i] = round_h(static_cast<float>(h[k][i]) + static_cast<float>(d[i]));
         *reinterpret_cast<half8_t*>(p) = h[k];
@@ -244,18 +279,18 @@ __global__ __launch_bounds__(kSiluThreads) void silu_mul_kernel(_Float16* __rest
 
 extern "C" {
 
-int pc_rope_kv_append(void* query_out, void* key_out, void* value_out, const void* qkv, int64_t qkv_stride,
-                      const int64_t* positions, const void* rope_table, int32_t rope_positions, void* pool,
-                      int64_t num_blocks, int32_t layer, const int64_t* slot_mapping, int64_t num_tokens,
-                      void* stream) {
-  if (num_tokens < 0) return set_error(PC_ERR_ARGUMENT, "negative token count");
-  if (num_tokens > INT32_MAX) return set_error(PC_ERR_ARGUMENT, "too many tokens");
-  if (num_tokens == 0) return ok();  // nothing to read or write (empty buffers may be null)
-  if (!query_out || !qkv || !positions || !rope_table) return set_error(PC_ERR_ARGUMENT, "null pointer");
+}  // extern "C"
+
+namespace {
+
+// Shared by both RoPE entry points: exactly one of qkv / qkv_parts is given (checked by the
+// callers), with qkv_stride its row stride or split stride.
+int rope_kv_append(void* query_out, void* key_out, void* value_out, const void* qkv, const float* qkv_parts,
+                   int32_t splits, int64_t qkv_stride, const int64_t* positions, const void* rope_table,
+                   int32_t rope_positions, void* pool, int64_t num_blocks, int32_t layer,
+                   const int64_t* slot_mapping, int64_t num_tokens, void* stream) {
+  if (!query_out || !positions || !rope_table) return set_error(PC_ERR_ARGUMENT, "null pointer");
   if (rope_positions < 1) return set_error(PC_ERR_ARGUMENT, "rope_positions must be positive");
-  if (qkv_stride < kQkvElems || qkv_stride % 8 != 0)
-    return set_error(PC_ERR_ARGUMENT, "qkv_stride %lld must be >= %d and a multiple of 8",
-                     static_cast<long long>(qkv_stride), kQkvElems);
   if ((pool == nullptr) != (slot_mapping == nullptr))
     return set_error(PC_ERR_ARGUMENT, "pool and slot_mapping must both be given or both be null");
   if (pool != nullptr) {
@@ -263,14 +298,16 @@ int pc_rope_kv_append(void* query_out, void* key_out, void* value_out, const voi
       return set_error(PC_ERR_ARGUMENT, "num_blocks %lld out of range", static_cast<long long>(num_blocks));
     if (layer < 0 || layer >= kLayers) return set_error(PC_ERR_ARGUMENT, "layer %d outside [0, 22)", layer);
   }
-  if (!aligned(query_out, 16) || !aligned(qkv, 16) || !aligned(rope_table, 16) || !aligned(pool, 16) ||
-      !aligned(key_out, 16) || !aligned(value_out, 16))
+  if (!aligned(query_out, 16) || !aligned(qkv, 16) || !aligned(qkv_parts, 16) || !aligned(rope_table, 16) ||
+      !aligned(pool, 16) || !aligned(key_out, 16) || !aligned(value_out, 16))
     return set_error(PC_ERR_ARGUMENT, "buffers must be 16-byte aligned");
   RopeArgs a;
   a.query_out = static_cast<_Float16*>(query_out);
   a.key_out = static_cast<_Float16*>(key_out);
   a.value_out = static_cast<_Float16*>(value_out);
   a.qkv = static_cast<const _Float16*>(qkv);
+  a.qkv_parts = qkv_parts;
+  a.splits = splits;
   a.positions = positions;
   a.rope = static_cast<const _Float16*>(rope_table);
   a.pool = static_cast<_Float16*>(pool);
@@ -285,8 +322,8 @@ int pc_rope_kv_append(void* query_out, void* key_out, void* value_out, const voi
   return check_launch("rope_kv_append");
 }
 
-int pc_add_rms_norm(void* out, void* hidden, const void* delta, const void* weight, int64_t rows, int32_t width,
-                    float eps, void* stream) {
+int add_rms_norm(void* out, void* hidden, const void* delta, const float* delta_parts, int32_t splits,
+                 const void* weight, int64_t rows, int32_t width, float eps, void* stream) {
   if (rows < 0 || rows > INT32_MAX) return set_error(PC_ERR_ARGUMENT, "rows %lld out of range", static_cast<long long>(rows));
   if (width < 8 || width % 8 != 0 || width > kNormThreads * kNormMaxChunks * 8)
     return set_error(PC_ERR_ARGUMENT, "width %d must be a multiple of 8 in [8, %d]", width,
@@ -294,12 +331,59 @@ int pc_add_rms_norm(void* out, void* hidden, const void* delta, const void* weig
   if (rows == 0) return ok();  // nothing to read or write (empty buffers may be null)
   if (!out || !hidden || !weight) return set_error(PC_ERR_ARGUMENT, "null pointer");
   if (!(eps >= 0.0f)) return set_error(PC_ERR_ARGUMENT, "eps must be non-negative");
-  if (!aligned(out, 16) || !aligned(hidden, 16) || !aligned(delta, 16) || !aligned(weight, 16))
+  if (!aligned(out, 16) || !aligned(hidden, 16) || !aligned(delta, 16) || !aligned(delta_parts, 16) ||
+      !aligned(weight, 16))
     return set_error(PC_ERR_ARGUMENT, "buffers must be 16-byte aligned");
   hipLaunchKernelGGL(add_rms_norm_kernel, dim3(static_cast<uint32_t>(rows)), dim3(kNormThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<_Float16*>(out), static_cast<_Float16*>(hidden),
-                     static_cast<const _Float16*>(delta), static_cast<const _Float16*>(weight), width, eps);
+                     static_cast<const _Float16*>(delta), delta_parts, splits, rows * width,
+                     static_cast<const _Float16*>(weight), width, eps);
   return check_launch("add_rms_norm");
+}
+
+}  // namespace
+
+extern "C" {
+
+int pc_rope_kv_append(void* query_out, void* key_out, void* value_out, const void* qkv, int64_t qkv_stride,
+                      const int64_t* positions, const void* rope_table, int32_t rope_positions, void* pool,
+                      int64_t num_blocks, int32_t layer, const int64_t* slot_mapping, int64_t num_tokens,
+                      void* stream) {
+  if (num_tokens < 0) return set_error(PC_ERR_ARGUMENT, "negative token count");
+  if (num_tokens > INT32_MAX) return set_error(PC_ERR_ARGUMENT, "too many tokens");
+  if (num_tokens == 0) return ok();  // nothing to read or write (empty buffers may be null)
+  if (!qkv) return set_error(PC_ERR_ARGUMENT, "null pointer");
+  if (qkv_stride < kQkvElems || qkv_stride % 8 != 0)
+    return set_error(PC_ERR_ARGUMENT, "qkv_stride %lld must be >= %d and a multiple of 8",
+                     static_cast<long long>(qkv_stride), kQkvElems);
+  return rope_kv_append(query_out, key_out, value_out, qkv, nullptr, 1, qkv_stride, positions, rope_table,
+                        rope_positions, pool, num_blocks, layer, slot_mapping, num_tokens, stream);
+}
+
+int pc_rope_kv_append_parts(void* query_out, void* key_out, void* value_out, const float* qkv_parts, int32_t splits,
+                            const int64_t* positions, const void* rope_table, int32_t rope_positions, void* pool,
+                            int64_t num_blocks, int32_t layer, const int64_t* slot_mapping, int64_t num_tokens,
+                            void* stream) {
+  if (num_tokens < 0) return set_error(PC_ERR_ARGUMENT, "negative token count");
+  if (num_tokens > INT32_MAX / kQkvElems) return set_error(PC_ERR_ARGUMENT, "too many tokens");
+  if (num_tokens == 0) return ok();
+  if (!qkv_parts) return set_error(PC_ERR_ARGUMENT, "null pointer");
+  if (splits < 1 || splits > 64) return set_error(PC_ERR_ARGUMENT, "splits %d outside [1, 64]", splits);
+  return rope_kv_append(query_out, key_out, value_out, nullptr, qkv_parts, splits, num_tokens * kQkvElems, positions,
+                        rope_table, rope_positions, pool, num_blocks, layer, slot_mapping, num_tokens, stream);
+}
+
+int pc_add_rms_norm(void* out, void* hidden, const void* delta, const void* weight, int64_t rows, int32_t width,
+                    float eps, void* stream) {
+  return add_rms_norm(out, hidden, delta, nullptr, 1, weight, rows, width, eps, stream);
+}
+
+int pc_add_rms_norm_parts(void* out, void* hidden, const float* delta_parts, int32_t splits, const void* weight,
+                          int64_t rows, int32_t width, float eps, void* stream) {
+  if (rows > 0 && !delta_parts) return set_error(PC_ERR_ARGUMENT, "null pointer");
+  if (splits < 1 || splits > 64) return set_error(PC_ERR_ARGUMENT, "splits %d outside [1, 64]", splits);
+  if (rows > INT32_MAX / 8192) return set_error(PC_ERR_ARGUMENT, "rows %lld out of range", static_cast<long long>(rows));
+  return add_rms_norm(out, hidden, nullptr, delta_parts, splits, weight, rows, width, eps, stream);
 }
 
 int pc_silu_mul(void* out, const void* gate_up, int64_t rows, int32_t width, void* stream) {

@@ -62,7 +62,7 @@ using pc_internal::check_launch;
 using pc_internal::ok;
 using pc_internal::set_error;
 
-constexpr int kAbiVersion = 9;
+constexpr int kAbiVersion = 10;
 constexpr int kLayers = 22;
 constexpr int kSlots = 16;
 constexpr int kKVHeads = 4;

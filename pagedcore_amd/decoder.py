@@ -234,6 +234,68 @@ def _check_weights(weights: TinyLlamaWeights, what: str) -> None:
         raise ValueError(f"paged {what} requires 22 decoder layers")
 
 
+# Decode steps of up to GEMM_M128_ROWS rows run their q|k|v, o_proj, gate|up and down
+# projections on pc_gemm_m128: q|k|v, o_proj and down as fp32 split-K partial sums (summed
+# and rounded once by the RoPE / residual-add consumers), gate|up with the SwiGLU epilogue.
+# Shapes the kernel does not take (more rows, K not a multiple of 64, ...) use F.linear.
+GEMM_M128_ROWS = 128
+QKV_SPLITS = 4
+O_PROJ_SPLITS = 4
+DOWN_SPLITS = 8
+
+
+def _linear_parts(x: Tensor, weight: Tensor, preferred_splits: int) -> Tensor:
+    """x @ weight.T: fp32 split-K partial sums [splits, rows, n] from pc_gemm_m128 (the most
+    splits up to preferred_splits whose K ranges are multiples of 64), or the fp16 product
+    [rows, n] of F.linear when the shape does not fit that kernel."""
+    rows, k = x.shape
+    n = weight.shape[0]
+    if rows <= GEMM_M128_ROWS and n % 32 == 0 and x.is_contiguous() and weight.is_contiguous():
+        splits = preferred_splits
+        while splits >= 1:
+            if k % (64 * splits) == 0:
+                parts = torch.empty((splits, rows, n), dtype=torch.float32, device=x.device)
+                _hip.gemm_m128(parts, x, weight, splits=splits)
+                return parts
+            splits //= 2
+    return F.linear(x, weight)
+
+
+def _swiglu(x: Tensor, gate_up: Tensor) -> Tensor:
+    """fp16(fp16(silu(x @ gate.T)) * fp16(x @ up.T)) for the stacked [gate | up] weight:
+    one pc_gemm_m128 launch with the SwiGLU epilogue, or F.linear + pc_silu_mul."""
+    rows, k = x.shape
+    n = gate_up.shape[0]
+    activated = torch.empty((rows, n // 2), dtype=torch.float16, device=x.device)
+    if rows <= GEMM_M128_ROWS and n % 64 == 0 and k % 64 == 0 and x.is_contiguous() and gate_up.is_contiguous():
+        _hip.gemm_m128(activated, x, gate_up, epilogue=_hip.GEMM_SWIGLU)
+    else:
+        _hip.silu_mul(activated, F.linear(x, gate_up))
+    return activated
+
+
+def _add_rms_norm(x: Tensor, hidden: Tensor, delta: Tensor, weight: Tensor) -> None:
+    """hidden += delta; x = RMSNorm(hidden) * weight, for an fp16 delta or fp32 partial sums."""
+    if delta.ndim == 3:
+        _hip.add_rms_norm_parts(x, hidden, delta, weight, RMS_EPS)
+    else:
+        _hip.add_rms_norm(x, hidden, delta, weight, RMS_EPS)
+
+
+def _attention_block(
+    x: Tensor, hidden: Tensor, layer: LayerWeights, fused: _FusedLayer, following_norm: Tensor, attend
+) -> None:
+    """One decoder layer around its attention, in place on (x, hidden): q|k|v projection,
+    attend(qkv) -> attention [rows, 2048] (RoPE, KV write and paged attention, supplied by
+    the caller; qkv fp16 [rows, 2560] or fp32 partial sums [splits, rows, 2560]), o_proj +
+    residual + RMSNorm, SwiGLU MLP + residual + the next RMSNorm (reference
+    src/pagedcore/decoder.py:173-193)."""
+    attention = attend(_linear_parts(x, fused.qkv, QKV_SPLITS))
+    _add_rms_norm(x, hidden, _linear_parts(attention, layer.o_proj, O_PROJ_SPLITS), layer.post_attention_norm)
+    activated = _swiglu(x, fused.gate_up)
+    _add_rms_norm(x, hidden, _linear_parts(activated, layer.down_proj, DOWN_SPLITS), following_norm)
+
+
 def _check_gpu(allocator: KVAllocator, weights: TinyLlamaWeights, what: str) -> None:
     """The kernels run on the GPU only: fail before any staging when the pool or the
     weights live elsewhere (there is no CPU fallback)."""
@@ -270,18 +332,13 @@ def decode_paged(
         _hip.add_rms_norm(x, hidden, None, weights.layers[0].input_norm, RMS_EPS)
         batch = len(request_ids)
         for index, layer in enumerate(weights.layers):
-            fused = _fused(layer)
-            qkv = F.linear(x, fused.qkv)
-            query = allocator.write_decode_layers_rotary(request_ids, index, qkv, table)
-            attention = paged_attention_batch(query, allocator, request_ids, layer_index=index)
-            projected = F.linear(attention.view(batch, HIDDEN), layer.o_proj)
-            _hip.add_rms_norm(x, hidden, projected, layer.post_attention_norm, RMS_EPS)
-            gate_up = F.linear(x, fused.gate_up)
-            activated = torch.empty((batch, gate_up.shape[1] // 2), dtype=torch.float16, device=x.device)
-            _hip.silu_mul(activated, gate_up)
-            down = F.linear(activated, layer.down_proj)
+
+            def attend(qkv: Tensor, index: int = index) -> Tensor:
+                query = allocator.write_decode_layers_rotary(request_ids, index, qkv, table)
+                return paged_attention_batch(query, allocator, request_ids, layer_index=index).view(batch, HIDDEN)
+
             following = weights.layers[index + 1].input_norm if index + 1 < LAYERS else weights.final_norm
-            _hip.add_rms_norm(x, hidden, down, following, RMS_EPS)
+            _attention_block(x, hidden, layer, _fused(layer), following, attend)
         logits = F.linear(x, weights.lm_head)
     return logits.unsqueeze(1)
 
@@ -373,18 +430,17 @@ class DecodeGraph:
         query = torch.empty((batch, Q_HEADS, HEAD_DIM), dtype=torch.float16, device=pool.device)
         attention = torch.empty_like(query)
         for index, layer in enumerate(weights.layers):
-            fused = _fused(layer)
-            qkv = F.linear(x, fused.qkv)
-            _hip.rope_kv_append(query, qkv, positions, self._table, pool=pool, layer=index, slot_mapping=slots)
-            _hip.planned_decode_attention(attention, query, pool, index, self._lens, self._plan, MAX_BLOCKS, self._workspace)
-            projected = F.linear(attention.view(batch, HIDDEN), layer.o_proj)
-            _hip.add_rms_norm(x, hidden, projected, layer.post_attention_norm, RMS_EPS)
-            gate_up = F.linear(x, fused.gate_up)
-            activated = torch.empty((batch, gate_up.shape[1] // 2), dtype=torch.float16, device=pool.device)
-            _hip.silu_mul(activated, gate_up)
-            down = F.linear(activated, layer.down_proj)
+
+            def attend(qkv: Tensor, index: int = index) -> Tensor:
+                if qkv.ndim == 3:
+                    _hip.rope_kv_append_parts(query, qkv, positions, self._table, pool=pool, layer=index, slot_mapping=slots)
+                else:
+                    _hip.rope_kv_append(query, qkv, positions, self._table, pool=pool, layer=index, slot_mapping=slots)
+                _hip.planned_decode_attention(attention, query, pool, index, self._lens, self._plan, MAX_BLOCKS, self._workspace)
+                return attention.view(batch, HIDDEN)
+
             following = weights.layers[index + 1].input_norm if index + 1 < LAYERS else weights.final_norm
-            _hip.add_rms_norm(x, hidden, down, following, RMS_EPS)
+            _attention_block(x, hidden, layer, _fused(layer), following, attend)
         return F.linear(x, weights.lm_head)
 
     @torch.inference_mode()

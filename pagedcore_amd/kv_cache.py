@@ -109,7 +109,10 @@ class HipKVWriter:
         self, pool: Tensor, layer: int, qkv: Tensor, rope_table: Tensor, positions: Tensor, slots: Tensor,
         query_out: Tensor,
     ) -> None:
-        _hip.rope_kv_append(query_out, qkv, positions, rope_table, pool=pool, layer=layer, slot_mapping=slots)
+        if qkv.ndim == 3:  # fp32 split-K partial sums of the projection
+            _hip.rope_kv_append_parts(query_out, qkv, positions, rope_table, pool=pool, layer=layer, slot_mapping=slots)
+        else:
+            _hip.rope_kv_append(query_out, qkv, positions, rope_table, pool=pool, layer=layer, slot_mapping=slots)
 
 
 class _HostOnlyWriter:
@@ -530,7 +533,8 @@ class KVAllocator:
 
         qkv: FP16 [B, >= 2560] on the pool device, unit column stride: row b holds the
         query (32 x 64), key (4 x 64) and value (4 x 64) projections of request_ids[b]'s
-        new token. rope_table: FP16 [rope positions, 2, 32] cos/sin table. Row b's query and
+        new token; or the same projections as contiguous FP32 split-K partial sums
+        [splits, B, 2560] (pc_gemm_m128's output), rounded to FP16 once. rope_table: FP16 [rope positions, 2, 32] cos/sin table. Row b's query and
         key are rotated at the request's position (its cached length before this step, as
         the reference decoder passes it to apply_rope, src/pagedcore/decoder.py:173-186);
         the rotated key and the unrotated value go to the staged slot of this layer, like
@@ -548,7 +552,16 @@ class KVAllocator:
             raise ValueError("layer_index must identify one of the 22 decoder layers")
         if any(layer_index != append.written_layers for append in appends):
             raise ValueError("decode cache layers must be written once in order")
-        if (
+        if qkv.ndim == 3:
+            if (
+                qkv.shape[1:] != (len(request_ids), QKV_COLUMNS)
+                or not 1 <= qkv.shape[0] <= 64
+                or qkv.dtype != torch.float32
+                or not qkv.is_contiguous()
+                or qkv.device != self._pool.device
+            ):
+                raise ValueError("qkv partial sums must be contiguous FP32 [splits, batch, 2560] on the pool device")
+        elif (
             qkv.ndim != 2
             or qkv.shape[0] != len(request_ids)
             or qkv.shape[1] < QKV_COLUMNS

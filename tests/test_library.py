@@ -207,3 +207,48 @@ def test_noalloc_attention_refuses_oversize_shapes_before_any_hip_call():
     assert status == 1 and b"allocation-free entry point holds" in lib.pc_last_error()
     assert lib.pc_paged_decode_attn_noalloc(None, None, None, 8, 0, None, 1, 0, None, 1, None) == 1
     assert b"max_blocks" in lib.pc_last_error()
+
+
+@pytest.mark.parametrize(
+    "overrides,needle",
+    [
+        ({"out": None}, b"null pointer"),
+        ({"m": 0}, b"m = 0"),
+        ({"m": 129}, b"m = 129"),
+        ({"k": 2048, "splits": 3}, b"not divisible"),
+        ({"k": 96}, b"multiple of 64"),
+        ({"n": 48}, b"multiple of 32"),
+        ({"epilogue": 1, "splits": 2}, b"one split"),
+        ({"epilogue": 2, "splits": 2}, b"one split"),
+        ({"epilogue": 2, "n": 96, "splits": 1}, b"multiple of 64"),
+        ({"epilogue": 7}, b"unknown epilogue"),
+        ({"x": 264}, b"aligned"),
+        ({"n": 1 << 20, "k": 1 << 12}, b"too large"),
+    ],
+)
+def test_gemm_rejects_invalid_arguments_without_a_gpu(overrides, needle):
+    """pc_gemm_m128 validates shapes, splits, epilogue and alignment before any HIP call."""
+    lib = _hip.load()
+    a = {"out": 256, "x": 256, "w": 256, "m": 128, "n": 2048, "k": 2048, "splits": 4, "epilogue": 0}
+    a.update(overrides)
+    status = lib.pc_gemm_m128(a["out"], a["x"], a["w"], a["m"], a["n"], a["k"], a["splits"], a["epilogue"], None)
+    assert status == 1
+    assert needle in lib.pc_last_error()
+
+
+def test_split_k_consumers_reject_invalid_arguments_without_a_gpu():
+    lib = _hip.load()
+    assert lib.pc_add_rms_norm_parts(256, 256, None, 1, 256, 4, 2048, 1e-5, None) == 1
+    assert b"null pointer" in lib.pc_last_error()
+    assert lib.pc_add_rms_norm_parts(256, 256, 256, 0, 256, 4, 2048, 1e-5, None) == 1
+    assert b"splits" in lib.pc_last_error()
+    assert lib.pc_add_rms_norm_parts(256, 256, 264, 2, 256, 4, 2048, 1e-5, None) == 1
+    assert b"aligned" in lib.pc_last_error()
+    assert lib.pc_add_rms_norm_parts(256, 256, 256, 2, 256, 4, 2049, 1e-5, None) == 1
+    assert b"width" in lib.pc_last_error()
+    assert lib.pc_rope_kv_append_parts(256, None, None, None, 4, 256, 256, 2048, None, 0, 0, None, 3, None) == 1
+    assert b"null pointer" in lib.pc_last_error()
+    assert lib.pc_rope_kv_append_parts(256, None, None, 256, 65, 256, 256, 2048, None, 0, 0, None, 3, None) == 1
+    assert b"splits" in lib.pc_last_error()
+    assert lib.pc_rope_kv_append_parts(256, None, None, 256, 4, 256, 256, 2048, 256, 0, 0, None, 3, None) == 1
+    assert b"both" in lib.pc_last_error()
