@@ -719,17 +719,20 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_decode_attention_b64_hbm_tr
 EXTRA_CPU_SECONDS = 3.0  # CPU baseline sample of each extra workload that has one
 
 
+ATTENTION_SOURCES = ("pagedcore_hip.hip", "pc_device.h", "pc_internal.h")
+
+
 def kernel_source_hash() -> str:
-    """sha256 (first 16 hex digits) of the library's kernel sources, csrc/*.hip and *.h in
-    name order: the key under which a counter summary is valid."""
+    """sha256 (first 16 hex digits) of the sources the attention kernels are compiled from
+    (csrc/pagedcore_hip.hip and the device headers it includes, in that order): the key
+    under which the attention call's counter summary is valid."""
     import hashlib
 
     folder = os.path.join(ROOT, "pagedcore_amd", "csrc")
     digest = hashlib.sha256()
-    for name in sorted(os.listdir(folder)):
-        if name.endswith((".hip", ".h")):
-            with open(os.path.join(folder, name), "rb") as handle:
-                digest.update(name.encode() + b"\0" + handle.read())
+    for name in ATTENTION_SOURCES:
+        with open(os.path.join(folder, name), "rb") as handle:
+            digest.update(name.encode() + b"\0" + handle.read())
     return digest.hexdigest()[:16]
 
 
