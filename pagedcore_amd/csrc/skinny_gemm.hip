@@ -22,6 +22,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <math.h>
 #include <stdint.h>
 
@@ -240,6 +242,24 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_m128_kernel(GemmArgs a) {
   }
 }
 
+constexpr int kMaxDevices = 64;
+
+// Raises a kernel's dynamic LDS limit once per device (on the current one), remembering
+// the devices done in `done` (one bit each).
+int raise_lds_limit(const void* kernel, int bytes, std::atomic<uint64_t>& done) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+    return set_error(PC_ERR_LAUNCH, "cannot determine the current device");
+  }
+  const uint64_t bit = uint64_t{1} << device;
+  if (done.load(std::memory_order_acquire) & bit) return PC_OK;
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
+    return set_error(PC_ERR_LAUNCH, "cannot raise the GEMM's LDS limit to %d bytes", bytes);
+  }
+  done.fetch_or(bit, std::memory_order_acq_rel);
+  return PC_OK;
+}
+
 template <int NT, int KC, int STAGES, int WAVES, Epilogue E>
 int launch(GemmArgs a, int splits, hipStream_t s) {
   using S = Shape<NT, KC, STAGES, WAVES>;
@@ -247,12 +267,8 @@ int launch(GemmArgs a, int splits, hipStream_t s) {
     return set_error(PC_ERR_ARGUMENT, "k per split (%d) must be a multiple of %d", a.ksplit, KC);
   }
   auto kernel = gemm_m128_kernel<NT, KC, STAGES, WAVES, E>;
-  // Raising the dynamic LDS limit is idempotent; done on every call so that it holds for
-  // whichever device is current.
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS) !=
-      hipSuccess) {
-    return set_error(PC_ERR_LAUNCH, "cannot raise the GEMM's LDS limit to %d bytes", S::LDS);
-  }
+  static std::atomic<uint64_t> raised{0};
+  if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kernel), S::LDS, raised)) return rc;
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(a.tiles * splits)), dim3(64 * WAVES), S::LDS, s, a);
   return check_launch("gemm_m128");
 }
