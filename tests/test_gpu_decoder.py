@@ -916,3 +916,43 @@ def test_worker_streams_match_the_oracle_generate(device, graph_batch, prompt_gr
     print(f"worker vs oracle generate: {len(requests)} requests, {ties} near-tie choices", flush=True)
     counts = allocator.capacity()
     assert counts.owned_blocks == 0 and counts.reserved_blocks == 0 and counts.active_slots == 0
+
+
+@pytest.mark.parametrize("batch,expect_library_gemm", [(128, True), (130, False)])
+def test_decode_paged_projection_path_by_batch_size(device, monkeypatch, batch, expect_library_gemm):
+    """Up to 128 rows the step's projections run on pc_gemm_m128 (split-K partials summed by
+    the RoPE / residual kernels, SwiGLU fused); above that on F.linear. Both paths match the
+    contiguous fp32 decode (tests/unit/test_decoder.py:114-195 tolerances) on sampled rows."""
+    weights = _synthetic(device)
+    host_weights = _cpu(weights)
+    contexts = [3, 16, 17]
+    pool = torch.full((22, 2, 3 * batch, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    requests = tuple(RequestId(str(row)) for row in range(batch))
+    for row, request in enumerate(requests):
+        length = contexts[row % 3]
+        allocator.create(KVReservation(request, 3))
+        dec.prefill_paged(((torch.arange(length)[None] + row) % 31).to(device), weights, allocator, request)
+    calls = []
+    original = _hip.gemm_m128
+
+    def counting(*args, **kwargs):
+        calls.append(kwargs.get("epilogue", _hip.GEMM_PARTIALS))
+        return original(*args, **kwargs)
+
+    monkeypatch.setattr(_hip, "gemm_m128", counting)
+    tokens = torch.tensor([[(5 * row) % 31] for row in range(batch)])
+    sample = [0, 1, 2, batch // 2, batch - 1]
+    expected = {row: dref.decode_fp32(tokens[row : row + 1], _pool_cache(allocator, requests[row]), host_weights)
+                for row in sample}
+    logits = dec.decode_paged(tokens.to(device), weights, allocator, requests)
+    torch.cuda.synchronize()
+    if expect_library_gemm:
+        # per layer q|k|v, o_proj and gate|up (the synthetic MLP width 32 keeps down, whose
+        # K of 32 is not a multiple of 64, on F.linear)
+        assert calls.count(_hip.GEMM_PARTIALS) == 2 * 22 and calls.count(_hip.GEMM_SWIGLU) == 22
+    else:
+        assert calls == []
+    assert torch.isfinite(logits).all()
+    for row in sample:
+        torch.testing.assert_close(logits[row : row + 1].cpu(), expected[row][0], atol=5e-3, rtol=5e-3)
