@@ -11,17 +11,20 @@ decode step is one batch-wide pass per layer:
 
   x      = RMSNorm(embedding[ids])                           pc_add_rms_norm
   per layer:
-    qkv  = x @ [Wq; Wk; Wv]^T                                 fp16 GEMM (hipBLASLt via torch)
-    q    = RoPE(q); RoPE(k) and v -> the staged pool slots     pc_rope_kv_append
+    qkv  = x @ [Wq; Wk; Wv]^T                                 GEMM: fp32 split-K partials
+    q    = RoPE(q); RoPE(k) and v -> the staged pool slots     pc_rope_kv_append(_parts)
     a    = paged attention(q) over the request's blocks        pc_paged_decode_attn
-    h   += a @ Wo^T;  x = RMSNorm(h)                           GEMM, pc_add_rms_norm
-    m    = silu(x @ Wgate^T) * (x @ Wup^T)                     one GEMM on [Wgate; Wup], pc_silu_mul
-    h   += m @ Wdown^T; x = RMSNorm_next(h)                    GEMM, pc_add_rms_norm
-  logits = x @ Wlm^T                                          GEMM
+    h   += a @ Wo^T;  x = RMSNorm(h)                           GEMM partials, pc_add_rms_norm(_parts)
+    m    = silu(x @ Wgate^T) * (x @ Wup^T)                     one GEMM on [Wgate; Wup], SwiGLU epilogue
+    h   += m @ Wdown^T; x = RMSNorm_next(h)                    GEMM partials, pc_add_rms_norm(_parts)
+  logits = x @ Wlm^T                                          GEMM (hipBLASLt via torch)
 
-Every elementwise kernel rounds to fp16 where the reference's torch expression does (see
-the kernels' comments), so a row's result differs from the reference only by fp32
-summation order inside the GEMMs, the norms and the attention.
+The projections run on pc_gemm_m128 at up to 128 rows (the split-K partial sums are added
+and rounded to fp16 once by the kernel that consumes them) and on F.linear (hipBLASLt)
+otherwise, with pc_silu_mul for the SwiGLU. Every elementwise kernel rounds to fp16 where
+the reference's torch expression does (see the kernels' comments), so a row's result
+differs from the reference only by fp32 summation order inside the GEMMs, the norms and the
+attention.
 """
 
 from __future__ import annotations
