@@ -45,14 +45,36 @@ __device__ __forceinline__ _Float16 round_h(float x) { return static_cast<_Float
 
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
+constexpr int kUnrolledSplits = 8;  // split counts up to this load all their parts at once
+
 // fp16(sum over the splits of parts[s * split_stride + offset + 0..7]), added in split order.
+// Up to kUnrolledSplits splits, every load is issued before the first add (one memory round
+// trip, not one per split); a split past `splits` reloads split 0 and is not added.
 __device__ __forceinline__ half8_t sum_parts8(const float* parts, int64_t offset, int splits, int64_t split_stride) {
-  float4_t lo = *reinterpret_cast<const float4_t*>(parts + offset);
-  float4_t hi = *reinterpret_cast<const float4_t*>(parts + offset + 4);
-  for (int s = 1; s < splits; ++s) {
-    const float* p = parts + s * split_stride + offset;
-    lo += *reinterpret_cast<const float4_t*>(p);
-    hi += *reinterpret_cast<const float4_t*>(p + 4);
+  float4_t lo, hi;
+  if (splits <= kUnrolledSplits) {
+    float4_t l[kUnrolledSplits], h[kUnrolledSplits];
+#pragma unroll
+    for (int s = 0; s < kUnrolledSplits; ++s) {
+      const float* p = parts + (s < splits ? s : 0) * split_stride + offset;
+      l[s] = *reinterpret_cast<const float4_t*>(p);
+      h[s] = *reinterpret_cast<const float4_t*>(p + 4);
+    }
+    lo = l[0];
+    hi = h[0];
+#pragma unroll
+    for (int s = 1; s < kUnrolledSplits; ++s) {
+      lo = s < splits ? lo + l[s] : lo;
+      hi = s < splits ? hi + h[s] : hi;
+    }
+  } else {
+    lo = *reinterpret_cast<const float4_t*>(parts + offset);
+    hi = *reinterpret_cast<const float4_t*>(parts + offset + 4);
+    for (int s = 1; s < splits; ++s) {
+      const float* p = parts + s * split_stride + offset;
+      lo += *reinterpret_cast<const float4_t*>(p);
+      hi += *reinterpret_cast<const float4_t*>(p + 4);
+    }
   }
   half8_t out;
 #pragma unroll
