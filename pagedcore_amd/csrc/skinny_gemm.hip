@@ -59,6 +59,13 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
 }
+// Workgroup barrier without a memory fence (a fence would wait for every DMA in flight);
+// the empty asm statements keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 struct GemmArgs {
   const _Float16* x;
@@ -173,7 +180,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_m128_kernel(GemmArgs a) {
     // Every wave's DMA of stage t has landed, and every wave has finished reading stage
     // t - 1 (its LDS reads were consumed by its MFMAs), which the next DMA overwrites. A
     // bare barrier: a fence here would wait for the DMAs still in flight.
-    __builtin_amdgcn_s_barrier();
+    stage_barrier();
     if (t + STAGES - 1 < steps) {
       issue_stage<NT, KC, STAGES, WAVES, E>(smem + ((t + STAGES - 1) % STAGES) * S::SB, a, tile,
                                             k0 + (t + STAGES - 1) * KC, wave, lane);
