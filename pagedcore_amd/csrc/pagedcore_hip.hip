@@ -256,18 +256,29 @@ __device__ __forceinline__ float lane_value(float x, int k) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
 }
 
+// x of lane q (hi false) or of lane 4 + q (hi true). Both lanes are read in uniform control
+// flow and each lane then selects one: a readlane written inside the two arms of a per-lane
+// condition compiles to exec-masked branches around each read (about 0.3 us of the tail).
+__device__ __forceinline__ float lane_value_of_half(float x, int q, bool hi) {
+  const float lo_value = lane_value(x, q);
+  const float hi_value = lane_value(x, 4 + q);
+  return hi ? hi_value : lo_value;
+}
+
 // Online-softmax state of the 4 q heads a lane holds in the PV layout (q head 4(g&1) + r,
 // dims 16(2k + g/2) + c), with the fold of one more partial. Explicit fmaf: every fold
-// rounds the same way wherever it runs.
+// rounds the same way wherever it runs. The state starts as the first partial itself, which
+// is what folding that partial into the empty state (m = -inf, l = 0, O = 0) gives for any
+// partial with a finite m: scales exp2(-inf) = 0 and exp2(0) = 1, and fmaf(x, 1, 0) = x.
 struct Fold {
   float M[4], L[4], O[2][4];
-  __device__ __forceinline__ void init() {
+  __device__ __forceinline__ void set(const float (&m)[4], const float (&l)[4], const float (&x)[2][4]) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      M[r] = -INFINITY;
-      L[r] = 0.f;
-      O[0][r] = 0.f;
-      O[1][r] = 0.f;
+      M[r] = m[r];
+      L[r] = l[r];
+      O[0][r] = x[0][r];
+      O[1][r] = x[1][r];
     }
   }
   __device__ __forceinline__ void add(const float (&m)[4], const float (&l)[4], const float (&x)[2][4]) {
@@ -443,7 +454,7 @@ __global__ __launch_bounds__(kItemThreads) __attribute__((amdgpu_waves_per_eu(6,
       const float alpha = exp2_fast((m - mn) * kScoreToLog2);                                                   \
       lsum *= alpha;                                                                                            \
       float al[4];                                                                                              \
-      _Pragma("unroll") for (int q = 0; q < 4; ++q) al[q] = (g & 1) ? lane_value(alpha, 4 + q) : lane_value(alpha, q); \
+      _Pragma("unroll") for (int q = 0; q < 4; ++q) al[q] = lane_value_of_half(alpha, q, (g & 1) != 0); \
       _Pragma("unroll") for (int nt = 0; nt < 4; ++nt) _Pragma("unroll") for (int q = 0; q < 4; ++q) acc[nt][q] *= al[q]; \
       m = mn;                                                                                                   \
       mc = m * kScoreToLog2;                                                                                    \
@@ -493,12 +504,11 @@ __global__ __launch_bounds__(kItemThreads) __attribute__((amdgpu_waves_per_eu(6,
     for (int q = 0; q < 4; ++q) ox[k][q] = bad ? NAN : fold_low_rows(acc[2 * k][q], acc[2 * k + 1][q]);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    om[q] = (g & 1) ? lane_value(m, 4 + q) : lane_value(m, q);
-    ol[q] = (g & 1) ? lane_value(l, 4 + q) : lane_value(l, q);
+    om[q] = lane_value_of_half(m, q, (g & 1) != 0);
+    ol[q] = lane_value_of_half(l, q, (g & 1) != 0);
   }
 
   Fold f;
-  f.init();
   if (nsub > 1) {
     // Sub-chunk merge: every wave of kv head h leaves its partial in its own LDS area and
     // takes a ticket; the last one folds the head's sub-chunks in order.
@@ -508,16 +518,18 @@ __global__ __launch_bounds__(kItemThreads) __attribute__((amdgpu_waves_per_eu(6,
     if (lane == 0) old = __hip_atomic_fetch_add(&sub_tickets[h], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
     old = __builtin_amdgcn_readfirstlane(old);
     if (old != nsub - 1) return;
+    // Every sub-chunk's partial is read before the first fold (one LDS round trip; the
+    // area of a sub-chunk past nsub is read and not folded).
+    float px[kSubs][2][4], pm[kSubs][4], pl[kSubs][4];
 #pragma unroll
-    for (int s2 = 0; s2 < kSubs; ++s2) {
-      if (s2 < nsub) {
-        float px[2][4], pm[4], pl[4];
-        get_sub(lds + (h * kSubs + s2) * kAreaBytes, lane, g, px, pm, pl);
-        f.add(pm, pl, px);
-      }
+    for (int s2 = 0; s2 < kSubs; ++s2) get_sub(lds + (h * kSubs + s2) * kAreaBytes, lane, g, px[s2], pm[s2], pl[s2]);
+    f.set(pm[0], pl[0], px[0]);
+#pragma unroll
+    for (int s2 = 1; s2 < kSubs; ++s2) {
+      if (s2 < nsub) f.add(pm[s2], pl[s2], px[s2]);
     }
   } else {
-    f.add(om, ol, ox);
+    f.set(om, ol, ox);
   }
 
   if (nitems == 1) {
