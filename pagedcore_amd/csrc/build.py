@@ -40,6 +40,11 @@ FLAGS = [
     # uses them).
     "-mllvm",
     "-amdgpu-mfma-vgpr-form",
+    # Leading kernel arguments (up to 14 SGPRs) arrive in SGPRs at wave launch instead of
+    # through a scalar load of the argument buffer: one memory round trip less before a
+    # kernel's first dependent load.
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
     # Per-kernel register, scratch and occupancy report, checked below.
     "-Rpass-analysis=kernel-resource-usage",
 ]

@@ -349,7 +349,22 @@ __device__ __forceinline__ void store_natural(void* dst, char* area, int lane, c
 }
 
 __global__ __launch_bounds__(kItemThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void paged_decode_item_kernel(
-    AttnArgs a) {
+    const int32_t* plan, const _Float16* query, const _Float16* pool, int64_t num_blocks, int layer, int batch,
+    int max_blocks, int max_items, _Float16* out, float* partials) {
+  // Scalar parameters, those the first loads need leading: the compiler preloads the leading
+  // ones into SGPRs at wave launch (no kernel-argument round trip before the plan record).
+  AttnArgs a;
+  a.out = out;
+  a.query = query;
+  a.pool = pool;
+  a.num_blocks = num_blocks;
+  a.plan = plan;
+  a.context_lens = nullptr;
+  a.partials = partials;
+  a.layer = layer;
+  a.batch = batch;
+  a.max_blocks = max_blocks;
+  a.max_items = max_items;
   __shared__ __attribute__((aligned(16))) char lds[kItemWaves * kAreaBytes];
   __shared__ int32_t sub_tickets[kKVHeads];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -550,7 +565,15 @@ __global__ __launch_bounds__(kItemThreads) __attribute__((amdgpu_waves_per_eu(6,
 // Merge of multi-item sequences: one workgroup per (sequence, kv head); thread t owns dims
 // 2(t % 32), +1 of q head t / 32 and folds the items' partials in item order, the loads of
 // up to kMergeItems items issued at once.
-__global__ __launch_bounds__(kMergeThreads) void paged_decode_merge_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kMergeThreads) void paged_decode_merge_kernel(const int32_t* context_lens, int max_blocks,
+                                                                         int max_items, const float* partials,
+                                                                         _Float16* out) {
+  AttnArgs a;
+  a.out = out;
+  a.context_lens = context_lens;
+  a.partials = const_cast<float*>(partials);
+  a.max_blocks = max_blocks;
+  a.max_items = max_items;
   const int grp = blockIdx.x;
   const int b = grp / kKVHeads, h = grp % kKVHeads;
   const int t = threadIdx.x;
@@ -796,11 +819,12 @@ int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t
   a.max_items = static_cast<int>(max_items);
   hipStream_t s = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
-  hipLaunchKernelGGL(paged_decode_item_kernel, dim3(static_cast<unsigned>(num_records)), dim3(kItemThreads), 0, s, a);
+  hipLaunchKernelGGL(paged_decode_item_kernel, dim3(static_cast<unsigned>(num_records)), dim3(kItemThreads), 0, s, a.plan,
+                     a.query, a.pool, a.num_blocks, a.layer, a.batch, a.max_blocks, a.max_items, a.out, a.partials);
   if (int rc = check_launch("paged_decode_item")) return rc;
   if (max_items > 1) {
     hipLaunchKernelGGL(paged_decode_merge_kernel, dim3(static_cast<unsigned>(batch) * kKVHeads), dim3(kMergeThreads), 0,
-                       s, a);
+                       s, a.context_lens, a.max_blocks, a.max_items, static_cast<const float*>(a.partials), a.out);
     return check_launch("paged_decode_merge");
   }
   return PC_OK;
