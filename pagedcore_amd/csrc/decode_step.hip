@@ -142,7 +142,28 @@ __device__ __forceinline__ half8_t load_qkv8(const RopeArgs& a, int64_t t, int c
   return *reinterpret_cast<const half8_t*>(a.qkv + t * a.qkv_stride + col);
 }
 
-__global__ __launch_bounds__(kRopeThreads) void rope_kv_append_kernel(RopeArgs a) {
+// Scalar parameters, those the first loads need leading (the compiler preloads the leading
+// 56 bytes into SGPRs at wave launch: no kernel-argument round trip before them).
+__global__ __launch_bounds__(kRopeThreads) void rope_kv_append_kernel(
+    const int64_t* positions, const float* qkv_parts, const _Float16* qkv, int64_t qkv_stride, const _Float16* rope,
+    const int64_t* slot_mapping, int32_t splits, int32_t rope_positions, _Float16* pool, int64_t slot_limit,
+    int64_t kind_elems, _Float16* query_out, _Float16* key_out, _Float16* value_out, int32_t layer) {
+  RopeArgs a;
+  a.query_out = query_out;
+  a.key_out = key_out;
+  a.value_out = value_out;
+  a.qkv = qkv;
+  a.qkv_parts = qkv_parts;
+  a.splits = splits;
+  a.positions = positions;
+  a.rope = rope;
+  a.pool = pool;
+  a.slot_mapping = slot_mapping;
+  a.qkv_stride = qkv_stride;
+  a.slot_limit = slot_limit;
+  a.kind_elems = kind_elems;
+  a.layer = layer;
+  a.rope_positions = rope_positions;
   const int64_t t = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t position = a.positions[t];
@@ -212,14 +233,15 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 // delta, when given, is fp16 [rows][width] or (delta_parts, splits) fp32 partial sums
-// [splits][rows][width], rounded to fp16 before the add.
-__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(_Float16* __restrict__ out,
-                                                                    _Float16* __restrict__ hidden,
-                                                                    const _Float16* __restrict__ delta,
+// [splits][rows][width], rounded to fp16 before the add. The parameters the first loads need
+// lead (they are preloaded into SGPRs).
+__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(_Float16* __restrict__ hidden,
                                                                     const float* __restrict__ delta_parts,
-                                                                    int32_t splits, int64_t parts_stride,
+                                                                    const _Float16* __restrict__ delta,
+                                                                    int64_t parts_stride, int32_t splits,
+                                                                    int32_t width, float eps,
                                                                     const _Float16* __restrict__ weight,
-                                                                    int32_t width, float eps) {
+                                                                    _Float16* __restrict__ out) {
 #pragma clang fp contract(off)
   __shared__ float wave_sums[kNormThreads / 64];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * width;
@@ -323,24 +345,12 @@ int rope_kv_append(void* query_out, void* key_out, void* value_out, const void* 
   if (!aligned(query_out, 16) || !aligned(qkv, 16) || !aligned(qkv_parts, 16) || !aligned(rope_table, 16) ||
       !aligned(pool, 16) || !aligned(key_out, 16) || !aligned(value_out, 16))
     return set_error(PC_ERR_ARGUMENT, "buffers must be 16-byte aligned");
-  RopeArgs a;
-  a.query_out = static_cast<_Float16*>(query_out);
-  a.key_out = static_cast<_Float16*>(key_out);
-  a.value_out = static_cast<_Float16*>(value_out);
-  a.qkv = static_cast<const _Float16*>(qkv);
-  a.qkv_parts = qkv_parts;
-  a.splits = splits;
-  a.positions = positions;
-  a.rope = static_cast<const _Float16*>(rope_table);
-  a.pool = static_cast<_Float16*>(pool);
-  a.slot_mapping = slot_mapping;
-  a.qkv_stride = qkv_stride;
-  a.slot_limit = pool ? num_blocks * kSlots : 0;
-  a.kind_elems = pool ? num_blocks * kSlots * kRowElems : 0;
-  a.layer = pool ? layer : 0;
-  a.rope_positions = rope_positions;
   hipLaunchKernelGGL(rope_kv_append_kernel, dim3(static_cast<uint32_t>(num_tokens)), dim3(kRopeThreads), 0,
-                     static_cast<hipStream_t>(stream), a);
+                     static_cast<hipStream_t>(stream), positions, qkv_parts, static_cast<const _Float16*>(qkv),
+                     qkv_stride, static_cast<const _Float16*>(rope_table), slot_mapping, splits, rope_positions,
+                     static_cast<_Float16*>(pool), pool ? num_blocks * kSlots : int64_t{0},
+                     pool ? num_blocks * kSlots * kRowElems : int64_t{0}, static_cast<_Float16*>(query_out),
+                     static_cast<_Float16*>(key_out), static_cast<_Float16*>(value_out), pool ? layer : 0);
   return check_launch("rope_kv_append");
 }
 
@@ -357,9 +367,9 @@ int add_rms_norm(void* out, void* hidden, const void* delta, const float* delta_
       !aligned(weight, 16))
     return set_error(PC_ERR_ARGUMENT, "buffers must be 16-byte aligned");
   hipLaunchKernelGGL(add_rms_norm_kernel, dim3(static_cast<uint32_t>(rows)), dim3(kNormThreads), 0,
-                     static_cast<hipStream_t>(stream), static_cast<_Float16*>(out), static_cast<_Float16*>(hidden),
-                     static_cast<const _Float16*>(delta), delta_parts, splits, rows * width,
-                     static_cast<const _Float16*>(weight), width, eps);
+                     static_cast<hipStream_t>(stream), static_cast<_Float16*>(hidden), delta_parts,
+                     static_cast<const _Float16*>(delta), rows * width, splits, width, eps,
+                     static_cast<const _Float16*>(weight), static_cast<_Float16*>(out));
   return check_launch("add_rms_norm");
 }
 

@@ -85,17 +85,23 @@ struct AppendChunk {
   int64_t dst;  // destination in 16 B units, -1 = nothing to store
 };
 
+// The kernel's arguments. The first 56 bytes (pointers, layer strides, token strides,
+// counts: everything the first loads need) are the ones the compiler preloads into SGPRs.
 struct AppendArgs {
   const char* key;
   const char* value;
   const int64_t* slot_mapping;
-  int64_t key_layer_bytes, key_token_bytes, value_layer_bytes, value_token_bytes;
+  int64_t key_layer_bytes, value_layer_bytes;
+  int32_t key_token_bytes, value_token_bytes;
+  uint32_t num_tokens, total_rows;
+  uint4* pool;
   int64_t slot_limit;
   int layer_begin;
-  uint32_t num_tokens, total_rows;
 };
 
-// Chunk q (16 B) of the flattened work: q = ((l * T + t) * 2 + kind) * 32 + c.
+// Chunk q (16 B) of the flattened work: q = ((l * T + t) * 2 + kind) * 32 + c. The source
+// chunk and the slot are loaded together (the source address does not depend on the slot),
+// so the chunk costs one memory round trip before its store.
 __device__ __forceinline__ AppendChunk append_load(const AppendArgs& a, uint32_t q) {
   AppendChunk out;
   out.dst = -1;
@@ -106,11 +112,11 @@ __device__ __forceinline__ AppendChunk append_load(const AppendArgs& a, uint32_t
     const uint32_t rest = row >> 1;
     const uint32_t t = rest % a.num_tokens;
     const uint32_t l = rest / a.num_tokens;
+    const char* src = kind ? a.value + l * a.value_layer_bytes + static_cast<int64_t>(t) * a.value_token_bytes
+                           : a.key + l * a.key_layer_bytes + static_cast<int64_t>(t) * a.key_token_bytes;
+    out.data = *reinterpret_cast<const uint4*>(src + c * 16);
     const int64_t slot = a.slot_mapping[t];
     if (slot >= 0 && slot < a.slot_limit) {
-      const char* src = kind ? a.value + l * a.value_layer_bytes + t * a.value_token_bytes
-                             : a.key + l * a.key_layer_bytes + t * a.key_token_bytes;
-      out.data = *reinterpret_cast<const uint4*>(src + c * 16);
       // pool row (layer, kind, slot) in units of one 512 B row, then the chunk.
       out.dst = ((static_cast<int64_t>(a.layer_begin + l) * 2 + kind) * a.slot_limit + slot) *
                     kRowChunks + c;
@@ -119,9 +125,14 @@ __device__ __forceinline__ AppendChunk append_load(const AppendArgs& a, uint32_t
   return out;
 }
 
-// Each thread moves four 16 B chunks, issuing all loads before any store.
-__global__ __launch_bounds__(kAppendThreads) void kv_append_vec_kernel(uint4* __restrict__ pool,
-                                                                       AppendArgs a) {
+// Each thread moves four 16 B chunks, issuing all loads before any store. Scalar parameters
+// in the order of AppendArgs, so that the leading ones are preloaded.
+__global__ __launch_bounds__(kAppendThreads) void kv_append_vec_kernel(
+    const char* key, const char* value, const int64_t* slot_mapping, int64_t key_layer_bytes,
+    int64_t value_layer_bytes, int32_t key_token_bytes, int32_t value_token_bytes, uint32_t num_tokens,
+    uint32_t total_rows, uint4* __restrict__ pool, int64_t slot_limit, int layer_begin) {
+  const AppendArgs a{key, value, slot_mapping, key_layer_bytes, value_layer_bytes, key_token_bytes, value_token_bytes,
+                     num_tokens, total_rows, pool, slot_limit, layer_begin};
   const uint32_t first = blockIdx.x * (kAppendThreads * kAppendChunksPerThread) + threadIdx.x;
   const AppendChunk c0 = append_load(a, first);
   const AppendChunk c1 = append_load(a, first + kAppendThreads);
@@ -757,25 +768,16 @@ int pc_kv_append(void* pool, int64_t num_blocks, int32_t layer_begin, int32_t nu
   hipStream_t s = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   const bool vec = aligned(key, 16) && aligned(value, 16) && kl % 16 == 0 && kt % 16 == 0 &&
-                   vl % 16 == 0 && vt % 16 == 0;
+                   vl % 16 == 0 && vt % 16 == 0 && kt >= INT32_MIN && kt <= INT32_MAX && vt >= INT32_MIN &&
+                   vt <= INT32_MAX;
   if (vec) {
     const uint64_t chunks = rows * kRowChunks;
     const uint64_t per_block = kAppendThreads * kAppendChunksPerThread;
     const unsigned grid = static_cast<unsigned>((chunks + per_block - 1) / per_block);
-    AppendArgs a;
-    a.key = static_cast<const char*>(key);
-    a.value = static_cast<const char*>(value);
-    a.slot_mapping = slot_mapping;
-    a.key_layer_bytes = kl;
-    a.key_token_bytes = kt;
-    a.value_layer_bytes = vl;
-    a.value_token_bytes = vt;
-    a.slot_limit = num_blocks * kSlots;
-    a.layer_begin = layer_begin;
-    a.num_tokens = static_cast<uint32_t>(num_tokens);
-    a.total_rows = static_cast<uint32_t>(rows);
-    hipLaunchKernelGGL(kv_append_vec_kernel, dim3(grid), dim3(kAppendThreads), 0, s,
-                       static_cast<uint4*>(pool), a);
+    hipLaunchKernelGGL(kv_append_vec_kernel, dim3(grid), dim3(kAppendThreads), 0, s, static_cast<const char*>(key),
+                       static_cast<const char*>(value), slot_mapping, kl, vl, static_cast<int32_t>(kt),
+                       static_cast<int32_t>(vt), static_cast<uint32_t>(num_tokens), static_cast<uint32_t>(rows),
+                       static_cast<uint4*>(pool), num_blocks * kSlots, layer_begin);
   } else {
     if (!aligned(key, 2) || !aligned(value, 2)) return set_error(PC_ERR_ARGUMENT, "K/V must be 2-byte aligned");
     const uint64_t words = rows * kRowElems;

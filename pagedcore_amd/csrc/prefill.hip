@@ -69,14 +69,18 @@ __device__ __forceinline__ half8_t join(short4_t x, short4_t y) {
 }
 
 struct PrefillArgs {
-  _Float16* out;
   const _Float16* q;
   const _Float16* k;
   const _Float16* v;
   int tokens;
+  _Float16* out;
 };
 
-__global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillArgs a) {
+// Scalar parameters in the order of PrefillArgs: all are preloaded into SGPRs at wave
+// launch.
+__global__ __launch_bounds__(kThreads) void prefill_attention_kernel(const _Float16* q, const _Float16* k,
+                                                                     const _Float16* v, int tokens, _Float16* out) {
+  const PrefillArgs a{q, k, v, tokens, out};
   // Two stages of kStepBlocks key blocks each: stage s, block b: K tile at s * kStageBytes +
   // b * kBufBytes, its V tile kTileBytes after it.
   __shared__ __attribute__((aligned(16))) char lds[2][kStageBytes];
@@ -245,9 +249,9 @@ extern "C" int pc_prefill_attention(void* out, const void* query, const void* ke
   if (!out || !query || !key || !value) return set_error(PC_ERR_ARGUMENT, "null pointer");
   if (!aligned(out, 16) || !aligned(query, 16) || !aligned(key, 16) || !aligned(value, 16))
     return set_error(PC_ERR_ARGUMENT, "buffers must be 16-byte aligned");
-  PrefillArgs a{static_cast<_Float16*>(out), static_cast<const _Float16*>(query), static_cast<const _Float16*>(key),
-                static_cast<const _Float16*>(value), tokens};
   const unsigned grid = static_cast<unsigned>((tokens + kBlock - 1) / kBlock) * kKVHeads;
-  hipLaunchKernelGGL(prefill_attention_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(prefill_attention_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const _Float16*>(query), static_cast<const _Float16*>(key),
+                     static_cast<const _Float16*>(value), static_cast<int>(tokens), static_cast<_Float16*>(out));
   return check_launch("prefill_attention");
 }

@@ -70,10 +70,10 @@ __device__ __forceinline__ void stage_barrier() {
 struct GemmArgs {
   const _Float16* x;
   const _Float16* w;
-  void* out;
   int m, n, k, ksplit;  // ksplit: K range of one split
   int tiles;            // workgroups per split
   int half_rows;        // SwiGLU: rows of gate_proj (up_proj starts there)
+  void* out;
 };
 
 template <int NT, int KC, int STAGES, int WAVES>
@@ -142,8 +142,12 @@ __device__ __forceinline__ void issue_stage(char* stage, const GemmArgs& a, int 
 
 __device__ __forceinline__ _Float16 round_h(float x) { return static_cast<_Float16>(x); }
 
+// Scalar parameters in the order of GemmArgs: all of them are preloaded into SGPRs at wave
+// launch (no kernel-argument round trip before the first DMA).
 template <int NT, int KC, int STAGES, int WAVES, Epilogue E>
-__global__ __launch_bounds__(64 * WAVES) void gemm_m128_kernel(GemmArgs a) {
+__global__ __launch_bounds__(64 * WAVES) void gemm_m128_kernel(const _Float16* x, const _Float16* w, int m, int n, int k,
+                                                               int ksplit, int tiles, int half_rows, void* out) {
+  const GemmArgs a{x, w, m, n, k, ksplit, tiles, half_rows, out};
   using S = Shape<NT, KC, STAGES, WAVES>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -276,7 +280,8 @@ int launch(GemmArgs a, int splits, hipStream_t s) {
   auto kernel = gemm_m128_kernel<NT, KC, STAGES, WAVES, E>;
   static std::atomic<uint64_t> raised{0};
   if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kernel), S::LDS, raised)) return rc;
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(a.tiles * splits)), dim3(64 * WAVES), S::LDS, s, a);
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(a.tiles * splits)), dim3(64 * WAVES), S::LDS, s, a.x, a.w, a.m,
+                     a.n, a.k, a.ksplit, a.tiles, a.half_rows, a.out);
   return check_launch("gemm_m128");
 }
 
