@@ -181,8 +181,9 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_word_kernel(
 //   * V, per block 16 rows x 128 B, straight into the wave's LDS area by LDS DMA
 //     (global_load_lds_dwordx4), each 32 B dim group of row r stored at group position
 //     u ^ sel(r) so that the transposing reads below are free of bank conflicts.
-// A CU holds two such workgroups (72 KiB of LDS and 77 VGPRs each), so a 64-sequence decode
-// batch is in flight in one round and HBM drains at its streaming rate.
+// K and V are read once per pass, so both use the non-temporal cache policy (the pool's
+// planes are far larger than the caches). A CU holds two such workgroups (72 KiB of LDS and
+// 77 VGPRs each), so a 64-sequence decode batch is in flight in one round.
 //
 // Per block (online softmax, fp32):
 //   * S^T[16 tokens][16] = K . Q^T on the matrix core (columns 8..15 repeat q heads 0..7):
@@ -442,10 +443,12 @@ __global__ __launch_bounds__(kItemThreads) __attribute__((amdgpu_waves_per_eu(6,
         id = 0;  // never dereferenced out of the pool
       }
       const _Float16* kb = lbase + static_cast<int64_t>(id) * kBlockElems;
-      load_pair(k0[t], k1[t], kb + c * kRowElems + 8 * g);
+      load_pair_stream(k0[t], k1[t], kb + c * kRowElems + 8 * g);
       const _Float16* vb = kb + kind_elems;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + offA), lds_ptr(area + t * kHeadBlockBytes), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + offB), lds_ptr(area + t * kHeadBlockBytes + 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + offA), lds_ptr(area + t * kHeadBlockBytes), 16, 0,
+                                       kStreamAux);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + offB), lds_ptr(area + t * kHeadBlockBytes + 1024), 16,
+                                       0, kStreamAux);
       __builtin_amdgcn_sched_barrier(0);  // keep the issue order the waits below count on
     }
   }
