@@ -4,9 +4,9 @@ Workload (the metric's configuration): batched one-token paged decode attention,
 32 query / 4 KV heads, head dim 64, fp16 KV with N(0,1) values, context lengths drawn
 uniformly from 1..2048 (partial last blocks included), fragmented block tables carved from
 a random permutation of an 8192-block pool, repeated over the pool's 22 layers. A step is
-one pass over the 22 layers (one pc_paged_decode_attn call per layer: the split-K item
-kernel, then the kernel that merges the items of multi-item sequences), with inputs
-resident in HBM; the 22 layer planes (1.48 GB of KV per step) exceed the 256 MB Infinity
+one pass over the 22 layers (one pc_paged_decode_attn call per layer: one kernel over
+balanced bins of the batch's blocks, sequences cut at a bin edge merged inside it), with
+inputs resident in HBM; the 22 layer planes (1.48 GB of KV per step) exceed the 256 MB Infinity
 Cache, so the bytes come from HBM.
 
 Printed as one JSON line: value = algorithmic HBM bytes per step x steps / wall time
@@ -70,7 +70,7 @@ class DecodeLayers:
         self.lib = _hip.load()
         self.max_blocks = int(w.tables.shape[1])
         nbytes = int(self.lib.pc_attn_workspace_bytes(w.batch, self.max_blocks))
-        self.workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        self.workspace = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
         # One decode plan per step, shared by the 22 layers (built from the host lengths,
         # like the block tables).
         self.plan = torch.from_numpy(_hip.decode_plan(w.lengths, w.tables)).to(device)
@@ -142,9 +142,9 @@ def run_decode(steps: int, warmup: int, use_graph: bool = True) -> dict:
     torch.cuda.synchronize(device)
     per_step = sorted(begin.elapsed_time(end) for begin, end in events)
     # The timed region holds steps x 22 pc_paged_decode_attn calls back to back on one
-    # stream (item kernel, then merge kernel, no host work in between when replayed as a
-    # graph), so its HIP-event time divided by the call count is the average call
-    # duration; rocprofv3's per-kernel averages of the two kernels add up to it.
+    # stream (one kernel launch each, no host work in between when replayed as a graph), so
+    # its HIP-event time divided by the call count is the average call duration (launch
+    # gaps included); rocprofv3's average kernel duration is that less the gap.
     launch_ms = total_ms / (steps * LAYERS)
     return {
         "layers": layers,
@@ -157,6 +157,7 @@ def run_decode(steps: int, warmup: int, use_graph: bool = True) -> dict:
         "launch_ms": launch_ms,
         "launch_gbps": bytes_per_launch / (launch_ms / 1e3) / 1e9,
         "graph": use_graph,
+        "bins": int((layers.plan[:, 0] > 0).sum().item()),
         "step_ms_median": per_step[len(per_step) // 2],
         "step_ms_min": per_step[0],
         "step_ms_max": per_step[-1],
@@ -249,7 +250,7 @@ def run_long_context(steps: int, warmup: int, cpu_seconds: float = 0.0) -> dict:
     max_blocks = int(w.tables.shape[1])
     lens = torch.from_numpy(w.lengths).to(device)
     plan = torch.from_numpy(_hip.decode_plan(w.lengths, w.tables)).to(device)
-    workspace = torch.empty(int(lib.pc_attn_workspace_bytes(w.batch, max_blocks)), dtype=torch.uint8, device=device)
+    workspace = torch.zeros(int(lib.pc_attn_workspace_bytes(w.batch, max_blocks)), dtype=torch.uint8, device=device)
     slots = torch.from_numpy(w.tables[:, max_blocks - 1].astype(np.int64) * 16 + 15).to(device)
     assert int(slots.max()) < w.num_blocks * 16
 
@@ -367,7 +368,7 @@ def run_single_decode(calls: int = 200, cpu_seconds: float = 0.0) -> dict:
     lib = _hip.load()
     plan = torch.from_numpy(_hip.decode_plan(lengths, table.numpy()[None])).to(device)
     lens = torch.from_numpy(lengths).to(device)
-    workspace = torch.empty(256, dtype=torch.uint8, device=device)
+    workspace = torch.zeros(int(lib.pc_attn_workspace_bytes(1, 8)), dtype=torch.uint8, device=device)
 
     def call() -> None:
         status = lib.pc_paged_decode_attn(
@@ -876,8 +877,8 @@ def main() -> int:
             "layers": LAYERS,
             "pool_blocks": w.num_blocks,
             "sum_context_tokens": int(w.lengths.sum()),
-            "blocks_per_work_item": 9,
-            "split_k_merge": "separate_kernel",
+            "attention_bins": int(r["bins"]),
+            "split_k_merge": "in_kernel (flags, same XCD)",
             "kv_dtype": "f16",
             "launch": "hip_graph" if r["graph"] else "eager",
         },
@@ -888,7 +889,7 @@ def main() -> int:
         "step_ms_max": round(r["step_ms_max"], 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "pc_paged_decode_attn: paged_decode_item_kernel + paged_decode_merge_kernel",
+            "kernel": "pc_paged_decode_attn: paged_decode_bin_kernel",
             "achieved": round(r["launch_gbps"], 2),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",

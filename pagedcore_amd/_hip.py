@@ -17,7 +17,7 @@ import numpy as np
 import torch
 from torch import Tensor
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 LIBRARY_NAME = "libpagedcore_hip.so"
 
 _lock = threading.Lock()
@@ -161,12 +161,13 @@ def _stream_key(device: torch.device) -> Tuple[int, int]:
 def attention_workspace(device: torch.device, nbytes: int) -> Tensor:
     """Split-K partial scratch for the current stream of `device`, grown on demand.
 
-    Reuse is safe because every call that uses it is ordered on that one stream.
+    Zero-initialized: the part flags in it must start at zero, and every call leaves them
+    so. Reuse is safe because every call that uses it is ordered on that one stream.
     """
     key = _stream_key(device)
     workspace = _workspaces.get(key)
     if workspace is None or workspace.numel() < nbytes:
-        workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        workspace = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
         _workspaces[key] = workspace
     return workspace
 
@@ -176,17 +177,20 @@ def workspace_bytes(batch: int, max_blocks: int) -> int:
 
 
 def plan_capacity(batch: int, max_blocks: int) -> int:
-    """Records pc_attn_plan may write for this shape (its pc_attn_plan_capacity)."""
+    """Plan rows pc_attn_plan may write for this shape (its pc_attn_plan_capacity)."""
     capacity = int(load().pc_attn_plan_capacity(batch, max_blocks))
     if capacity < 0:
         raise HipExtensionError(f"invalid attention shape batch={batch} max_blocks={max_blocks}")
     return capacity
 
 
-def decode_plan_into(context_lens: np.ndarray, block_tables: np.ndarray, plan: np.ndarray) -> int:
-    """pc_attn_plan into the caller's C-contiguous int32 [capacity, record ints] array
-    (capacity >= plan_capacity of the shape); records past the returned count become
-    empty padding records, so the whole array is a valid plan of `capacity` records."""
+def decode_plan_into(context_lens: np.ndarray, block_tables: np.ndarray, plan: np.ndarray,
+                     clear_to: Optional[int] = None) -> int:
+    """pc_attn_plan into the caller's C-contiguous int32 [capacity, row ints] array
+    (capacity >= plan_capacity of the shape). Rows past the returned count are made empty
+    padding rows up to `clear_to` (default: the whole array); a caller that knows how many
+    rows an earlier plan left in the array passes that count, and the whole array is then
+    a valid plan of `capacity` rows."""
     lib = load()
     lens = np.ascontiguousarray(context_lens, dtype=np.int32)
     tables = np.ascontiguousarray(block_tables, dtype=np.int32)
@@ -197,13 +201,13 @@ def decode_plan_into(context_lens: np.ndarray, block_tables: np.ndarray, plan: n
     count = int(lib.pc_attn_plan(lens.ctypes.data, tables.ctypes.data, lens.shape[0], tables.shape[1], plan.ctypes.data, plan.shape[0]))
     if count < 0:
         _check(lib, "pc_attn_plan", -count)
-    plan[count:] = 0
-    plan[count:, 0] = -1
+    end = plan.shape[0] if clear_to is None else min(max(clear_to, count), plan.shape[0])
+    plan[count:end] = 0
     return count
 
 
 def decode_plan(context_lens: np.ndarray, block_tables: np.ndarray) -> np.ndarray:
-    """Host decode plan: int32 [records, pc_attn_plan_record_ints()] from pc_attn_plan, built
+    """Host decode plan: int32 [rows, pc_attn_plan_record_ints()] from pc_attn_plan, built
     from HOST copies of the lengths [batch] and block tables [batch, max_blocks]."""
     lib = load()
     lens = np.ascontiguousarray(context_lens, dtype=np.int32)
@@ -239,8 +243,8 @@ def paged_decode_attention(
     out/query: fp16 [batch, 32, 64] contiguous; block_tables: int32 [batch, max_blocks];
     context_lens: int32 [batch] contiguous. All on the pool's device. `plan`: the
     decode_plan() rows for the same lengths and tables as a contiguous int32 device tensor
-    (None: built here from host copies, which synchronizes). `workspace` (uint8) defaults to
-    the per-stream cached buffer.
+    (None: built here from host copies, which synchronizes). `workspace` (uint8, zero before
+    its first use; every call leaves it so) defaults to the per-stream cached buffer.
     """
     lib = load()
     batch, max_blocks = block_tables.shape
@@ -259,8 +263,9 @@ def planned_decode_attention(
     workspace: Tensor,
 ) -> None:
     """pc_paged_decode_attn with a ready device plan (decode_plan() rows, possibly padded
-    with empty records) for a batch of context_lens.shape[0] rows whose tables are at most
-    max_blocks wide; workspace of workspace_bytes(batch, max_blocks) bytes."""
+    with empty rows) for a batch of context_lens.shape[0] rows whose tables are at most
+    max_blocks wide; workspace of workspace_bytes(batch, max_blocks) bytes, zero before its
+    first use (every call leaves it so)."""
     lib = load()
     batch = int(context_lens.shape[0])
     nbytes = int(lib.pc_attn_workspace_bytes(batch, max_blocks))

@@ -1,12 +1,13 @@
 """Compile libpagedcore_hip.so for gfx950 with hipcc (in-tree, next to the package).
 
 The build also checks the compiler's resource report of the kernels whose correctness
-depends on register allocation. The attention item kernel issues K loads and LDS reads as
-inline assembly that the compiler does not track, with hand-counted `vmcnt` waits: that is
-only correct while no register targeted by an outstanding load is copied, spilled or
-reused. A spill (scratch use) or a register budget above the occupancy the kernel was laid
-out for is the sign that this no longer holds, so such a build fails instead of producing a
-library whose outputs could be silently wrong.
+depends on register allocation or occupancy. The prompt attention kernel and the paged
+decode attention kernel issue loads and LDS reads as inline assembly that the compiler does
+not track, with hand-counted `vmcnt` waits: that is only correct while no register targeted
+by an outstanding load is copied, spilled or reused. The decode attention kernel also relies
+on two of its workgroups fitting one CU (empty plan rows then run beside the real ones). A
+spill (scratch use) or a register budget below the occupancy a kernel was laid out for fails
+the build instead of producing a library whose outputs or speed could silently change.
 """
 
 from __future__ import annotations
@@ -52,7 +53,7 @@ FLAGS = [
 # Kernels checked after every build: (demangled-name fragment) -> minimum waves per SIMD
 # the kernel's launch shape relies on. Each must report no scratch and no spills.
 GUARDED_KERNELS: Dict[str, int] = {
-    "paged_decode_item_kernel": 6,
+    "paged_decode_bin_kernel": 2,
     "prefill_attention_kernel": 6,
 }
 

@@ -62,7 +62,7 @@ using pc_internal::check_launch;
 using pc_internal::ok;
 using pc_internal::set_error;
 
-constexpr int kAbiVersion = 10;
+constexpr int kAbiVersion = 11;
 constexpr int kLayers = 22;
 constexpr int kSlots = 16;
 constexpr int kKVHeads = 4;
@@ -169,21 +169,25 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_word_kernel(
 }
 
 // ---------------------------------------------------------------------------------------
-// Paged decode attention.
+// Paged decode attention over balanced bins.
 //
-// Work split. A work item is 9 consecutive blocks of one sequence (the last item of a
-// sequence may hold fewer) and runs as one workgroup of 12 waves: wave w serves kv head
-// h = w % 4 for sub-chunk s = w / 4, i.e. blocks [9 item + 3 s, 9 item + 3 s + 3). Every
-// load of a wave is issued before its first block is processed:
-//   * Q of the head's 8 query heads (1 KiB, from L2 after the first item of the sequence);
-//   * K, per block 16 rows x 128 B: lane (c = lane % 16, g = lane / 16) loads row c, dims
-//     8g..8g+7 and 32+8g..39+8g -- the A operand of v_mfma_f32_16x16x32_f16 -- into VGPRs;
-//   * V, per block 16 rows x 128 B, straight into the wave's LDS area by LDS DMA
-//     (global_load_lds_dwordx4), each 32 B dim group of row r stored at group position
-//     u ^ sel(r) so that the transposing reads below are free of bank conflicts.
-// K and V are read once per pass, so both use the non-temporal cache policy (the pool's
-// planes are far larger than the caches). A CU holds two such workgroups (72 KiB of LDS and
-// 77 VGPRs each), so a 64-sequence decode batch is in flight in one round.
+// Work split. The host plan (pc_attn_plan) lays every sequence's blocks end to end and cuts
+// them into bins of nearly equal block counts, one workgroup per bin, so that every CU
+// streams the same number of bytes whatever the context lengths. Sequences are first dealt
+// to 8 groups (longest first, to the group with the fewest blocks); each group is cut into
+// its own bins, and bin i of group x is workgroup x + 8 i. The hardware dispatches
+// workgroup j to XCD (j + s) mod 8 for one s per launch, so all bins of one sequence run on
+// one XCD and share its L2. A bin holds at most kMaxSegs sequences (segments) and
+// kMaxUnits blocks; a sequence longer than the rest of a bin continues in the group's next
+// bin(s) (a cut sequence, spanning nspan bins).
+//
+// Each of the four waves streams one kv head's K and V of the bin's blocks, in bin order,
+// through a two-unit LDS ring filled by LDS DMA (global_load_lds_dwordx4, non-temporal: the
+// pool planes are read once per pass and are far larger than the caches). Q of each segment
+// is staged in LDS before the first unit. A (block, head) unit is 4 KiB: K as 16 rows of
+// 128 B, 16 B chunk q of row r at position q ^ (r & 7) (the reads below are free of bank
+// conflicts), then V with 32 B dim group u of row r at position u ^ row_sel(r) (for the
+// transposing reads).
 //
 // Per block (online softmax, fp32):
 //   * S^T[16 tokens][16] = K . Q^T on the matrix core (columns 8..15 repeat q heads 0..7):
@@ -196,47 +200,66 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_word_kernel(
 //   * O[16][64] += P . V with v_mfma_f32_16x16x16f16: rows 0..7 carry the fp16 rounding of
 //     p, rows 8..15 the remainder scaled by 2^18, so the product keeps fp32 accuracy over
 //     the range p in [2^-32, 2^8]; V reaches the B layout through ds_read_b64_tr_b16.
-// The three sub-chunk waves of a head then merge through LDS: each leaves (max, sum,
-// unnormalized O) in its area and takes an LDS ticket; the last one folds them in
-// sub-chunk order. A sequence that is one item writes its fp16 output directly; otherwise
-// the item's partial goes to the workspace and paged_decode_merge_kernel folds the items of
-// each (sequence, kv head) in item order.
+//
+// Outputs. A sequence complete within the bin is normalized into LDS during the stream and
+// written after it (no store shares the wave's memory counter with the ring's loads). A cut
+// sequence leaves one fp32 partial per bin and kv head in the workspace: every part but the
+// last is stored by its bin, which then raises the part's flag (after the stores are
+// acknowledged); the bin holding the last part (dispatched after all the others, so waiting
+// cannot deadlock) waits for the flags, folds the parts in span order with its own last,
+// writes the output and lowers the flags. Partials and flags stay in the XCD's L2 (plain
+// stores and loads are coherent there); the flag carries the writer's XCD id and a merge
+// that sees another XCD's id writes NaN rows instead of reading stale partials.
 // ---------------------------------------------------------------------------------------
 
-
-constexpr int kSubBlocks = 3;                              // blocks per wave
-constexpr int kSubs = 3;                                   // sub-chunk waves per kv head
-constexpr int kItemBlocks = kSubBlocks * kSubs;            // 9 blocks per work item
-constexpr int kItemWaves = kKVHeads * kSubs;               // 12 waves per workgroup
-constexpr int kItemThreads = 64 * kItemWaves;
-constexpr int kHeadBlockBytes = kSlots * kHeadDim * 2;     // one kv head of one block: 2 KiB
-constexpr int kAreaBytes = kSubBlocks * kHeadBlockBytes;   // LDS per wave: 6 KiB
-constexpr int kPlanInts = 16;                              // {seq, item, len, items, 9 ids, 3 x 0}
-constexpr int kPlanBins = 8;                               // XCDs of an MI355X
-constexpr int kPartFloats = kGroup * kHeadDim + 2 * kGroup;  // item partial: O [8][64], (m, l) x 8
-constexpr int kMergeThreads = 256;
-constexpr int kMergeItems = 16;                            // items per merge round trip
+constexpr int kBinThreads = 64 * kKVHeads;         // one wave per kv head
+constexpr int kRing = 2;                           // (block, head) units in flight per wave
+constexpr int kMaxSegs = 4;                        // sequences per bin
+constexpr int kMaxUnits = 256;                     // blocks per bin
+constexpr int kUnitBytes = 4096;                   // K (2 KiB) then V (2 KiB) of one head of one block
+constexpr int kWaveLds = kRing * kUnitBytes + 2 * kMaxSegs * 1024;  // ring, Q and output per segment
+constexpr int kHeaderInts = 8;                     // {segments, blocks, 0 x 6}
+constexpr int kSegInts = 8;                        // {sequence, length, first block, blocks, first bin, part, parts, first slot}
+constexpr int kRecordInts = kHeaderInts + kMaxSegs * kSegInts;
+constexpr int kRowInts = kRecordInts + kMaxUnits;  // one plan row: the record, then the block ids
+constexpr int kGroups = 8;                         // XCDs of an MI355X
+constexpr int kTargetBins = 256;                   // CUs of an MI355X
+constexpr int kMinBinBlocks = 8;                   // smaller workloads use fewer bins
+constexpr int kSlotBytes = 2176;                   // partial: O (2 KiB, lane-major), (m, l) x 8, flag; 17 lines
+constexpr int kFlagOffset = 2112;
+constexpr int kMaxSpins = 100000;                  // bounded wait for a part's flag
 // Scale of the low (remainder) part of p in the PV product (2^18).
 constexpr float kLowScale = 262144.0f;
 // Headroom (log2 of p) before the running max is raised.
 constexpr float kLazyLog2 = 8.0f;
-
-struct AttnArgs {
-  _Float16* out;
-  const _Float16* query;
-  const _Float16* pool;
-  int64_t num_blocks;
-  const int32_t* plan;
-  const int32_t* context_lens;
-  float* partials;  // [batch][4 kv heads][max_items][kPartFloats]
-  int layer, batch, max_blocks, max_items;
-};
+static_assert(kMaxUnits == 256, "the kernel reads a bin's block ids as four 64-lane vectors");
+static_assert(kRing == 2, "wait_ring covers one later unit");
 
 // Blocks holding `len` tokens, without the int32 overflow of len + 15.
 __device__ __host__ __forceinline__ int blocks_of(int len) { return len / kSlots + (len % kSlots != 0); }
 
-__device__ __forceinline__ int items_of(int len, int max_blocks) {
-  return len > 0 ? (min(blocks_of(len), max_blocks) + kItemBlocks - 1) / kItemBlocks : 0;
+// One uniform int32 by a scalar load that bypasses the scalar cache (sees L2; waits on
+// lgkmcnt only, so the ring's loads stay counted).
+__device__ __forceinline__ int sload_glc(const int32_t* p) {
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return v;
+}
+
+__device__ __forceinline__ int xcc_id() {
+  int v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xff;
+}
+
+// The ring's unit u has landed: at most `later` units (4 DMAs each) issued after it may be
+// outstanding. Loads return in order; no store is issued while the ring runs.
+__device__ __forceinline__ void wait_ring(int later) {
+  if (later > 0) {
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
 }
 
 // Reduce-scatter of a PV tile pair over the wave halves: lanes < 32 get x[l] + x[l + 32] / 2^18,
@@ -254,399 +277,419 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-
-// Every load of the wave has returned. The K registers are named so that none of them is
-// reused while a load of an unused block slot could still land in it.
-__device__ __forceinline__ void wait_all_loads(half8_t (&k0)[kSubBlocks], half8_t (&k1)[kSubBlocks]) {
-  asm volatile("s_waitcnt vmcnt(0)"
-               : "+v"(k0[0]), "+v"(k1[0]), "+v"(k0[1]), "+v"(k1[1]), "+v"(k0[2]), "+v"(k1[2])
-               :
-               : "memory");
-}
-
 __device__ __forceinline__ float lane_value(float x, int k) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
 }
 
 // x of lane q (hi false) or of lane 4 + q (hi true). Both lanes are read in uniform control
 // flow and each lane then selects one: a readlane written inside the two arms of a per-lane
-// condition compiles to exec-masked branches around each read (about 0.3 us of the tail).
+// condition compiles to exec-masked branches around each read.
 __device__ __forceinline__ float lane_value_of_half(float x, int q, bool hi) {
   const float lo_value = lane_value(x, q);
   const float hi_value = lane_value(x, 4 + q);
   return hi ? hi_value : lo_value;
 }
 
-// Online-softmax state of the 4 q heads a lane holds in the PV layout (q head 4(g&1) + r,
-// dims 16(2k + g/2) + c), with the fold of one more partial. Explicit fmaf: every fold
-// rounds the same way wherever it runs. The state starts as the first partial itself, which
-// is what folding that partial into the empty state (m = -inf, l = 0, O = 0) gives for any
-// partial with a finite m: scales exp2(-inf) = 0 and exp2(0) = 1, and fmaf(x, 1, 0) = x.
-struct Fold {
-  float M[4], L[4], O[2][4];
-  __device__ __forceinline__ void set(const float (&m)[4], const float (&l)[4], const float (&x)[2][4]) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      M[r] = m[r];
-      L[r] = l[r];
-      O[0][r] = x[0][r];
-      O[1][r] = x[1][r];
-    }
-  }
-  __device__ __forceinline__ void add(const float (&m)[4], const float (&l)[4], const float (&x)[2][4]) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float mn = fmaxf(M[r], m[r]);
-      const float so = exp2_fast((M[r] - mn) * kScoreToLog2);
-      const float sn = exp2_fast((m[r] - mn) * kScoreToLog2);
-      L[r] = fmaf(l[r], sn, L[r] * so);
-      O[0][r] = fmaf(x[0][r], sn, O[0][r] * so);
-      O[1][r] = fmaf(x[1][r], sn, O[1][r] * so);
-      M[r] = mn;
-    }
-  }
+// Partial of one (sequence, kv head) in the PV layout: lane (c, g) holds q heads 4(g&1)+r,
+// dims 16(2k + g/2) + c (k = 0, 1): unnormalized O, and the max and sum of each q head.
+struct Part {
+  float o[2][4];
+  float m[4], l[4];
 };
 
-// A sub-chunk partial in its wave's LDS area: lane L's 8 O values at [L][8] floats (value
-// (k, r) at 4k + r), then (m, l) of q head j at byte 2048 + 8j.
-__device__ __forceinline__ void put_sub(char* area, int lane, int g, const float (&x)[2][4], const float (&m)[4],
-                                        const float (&l)[4]) {
-  *reinterpret_cast<float4_t*>(area + lane * 32) = float4_t{x[0][0], x[0][1], x[0][2], x[0][3]};
-  *reinterpret_cast<float4_t*>(area + lane * 32 + 16) = float4_t{x[1][0], x[1][1], x[1][2], x[1][3]};
-  if (lane == 0 || lane == 16) {
-    *reinterpret_cast<float4_t*>(area + 2048 + (g & 1) * 32) = float4_t{m[0], l[0], m[1], l[1]};
-    *reinterpret_cast<float4_t*>(area + 2048 + (g & 1) * 32 + 16) = float4_t{m[2], l[2], m[3], l[3]};
-  }
-}
-
-__device__ __forceinline__ void get_sub(const char* area, int lane, int g, float (&x)[2][4], float (&m)[4], float (&l)[4]) {
-  const float4_t x0 = *reinterpret_cast<const float4_t*>(area + lane * 32);
-  const float4_t x1 = *reinterpret_cast<const float4_t*>(area + lane * 32 + 16);
-  const float4_t y0 = *reinterpret_cast<const float4_t*>(area + 2048 + (g & 1) * 32);
-  const float4_t y1 = *reinterpret_cast<const float4_t*>(area + 2048 + (g & 1) * 32 + 16);
+// acc <- acc (+) p, the online-softmax fold. Explicit fmaf: every fold rounds the same way
+// wherever it runs.
+__device__ __forceinline__ void fold_part(Part& acc, const Part& p) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    x[0][r] = x0[r];
-    x[1][r] = x1[r];
+    const float mn = fmaxf(acc.m[r], p.m[r]);
+    const float so = exp2_fast((acc.m[r] - mn) * kScoreToLog2);
+    const float sn = exp2_fast((p.m[r] - mn) * kScoreToLog2);
+    acc.l[r] = fmaf(p.l[r], sn, acc.l[r] * so);
+    acc.o[0][r] = fmaf(p.o[0][r], sn, acc.o[0][r] * so);
+    acc.o[1][r] = fmaf(p.o[1][r], sn, acc.o[1][r] * so);
+    acc.m[r] = mn;
   }
-  m[0] = y0[0]; l[0] = y0[1]; m[1] = y0[2]; l[1] = y0[3];
-  m[2] = y1[0]; l[2] = y1[1]; m[3] = y1[2]; l[3] = y1[3];
 }
 
-// PV-layout values to natural order [8 q heads][64] through `area`: the fp16 output rows
-// (scaled by inv[r]) or the fp32 item partial; each lane then stores 16 or 32 contiguous bytes.
-template <bool kHalf>
-__device__ __forceinline__ void store_natural(void* dst, char* area, int lane, const float (&x)[2][4], const float (&inv)[4]) {
+// fp16 output rows [8 q heads][64] of a partial, normalized, in natural order into `area`.
+__device__ __forceinline__ void put_output(char* area, int lane, const Part& p) {
   const int c = lane & 15, g = lane >> 4;
-  wave_lds_fence();
 #pragma unroll
   for (int k = 0; k < 2; ++k)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int idx = (4 * (g & 1) + r) * kHeadDim + 16 * (2 * k + (g >> 1)) + c;
-      if constexpr (kHalf) {
-        reinterpret_cast<_Float16*>(area)[idx] = static_cast<_Float16>(x[k][r] * inv[r]);
-      } else {
-        reinterpret_cast<float*>(area)[idx] = x[k][r];
-      }
+      reinterpret_cast<_Float16*>(area)[idx] = static_cast<_Float16>(p.o[k][r] * (1.0f / p.l[r]));
     }
-  wave_lds_fence();
-  char* d = static_cast<char*>(dst);
-  if constexpr (kHalf) {
-    *reinterpret_cast<uint4*>(d + lane * 16) = *reinterpret_cast<const uint4*>(area + lane * 16);
-  } else {
-    *reinterpret_cast<uint4*>(d + lane * 32) = *reinterpret_cast<const uint4*>(area + lane * 32);
-    *reinterpret_cast<uint4*>(d + lane * 32 + 16) = *reinterpret_cast<const uint4*>(area + lane * 32 + 16);
+}
+
+// A partial in a workspace slot: lane L's 8 O values at byte 32 L, then (m[4], l[4]) of q
+// heads 0..3 at 2048 and of q heads 4..7 at 2080; the part's flag word at kFlagOffset.
+__device__ __forceinline__ void store_part(char* slot, int lane, const Part& p) {
+  float4_t* d = reinterpret_cast<float4_t*>(slot + lane * 32);
+  d[0] = float4_t{p.o[0][0], p.o[0][1], p.o[0][2], p.o[0][3]};
+  d[1] = float4_t{p.o[1][0], p.o[1][1], p.o[1][2], p.o[1][3]};
+  if (lane == 0 || lane == 16) {
+    float4_t* e = reinterpret_cast<float4_t*>(slot + 2048 + (lane >> 4) * 32);
+    e[0] = float4_t{p.m[0], p.m[1], p.m[2], p.m[3]};
+    e[1] = float4_t{p.l[0], p.l[1], p.l[2], p.l[3]};
   }
 }
 
-__global__ __launch_bounds__(kItemThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void paged_decode_item_kernel(
-    const int32_t* plan, const _Float16* query, const _Float16* pool, int64_t num_blocks, int layer, int batch,
-    int max_blocks, int max_items, _Float16* out, float* partials) {
-  // Scalar parameters, those the first loads need leading: the compiler preloads the leading
-  // ones into SGPRs at wave launch (no kernel-argument round trip before the plan record).
-  AttnArgs a;
-  a.out = out;
-  a.query = query;
-  a.pool = pool;
-  a.num_blocks = num_blocks;
-  a.plan = plan;
-  a.context_lens = nullptr;
-  a.partials = partials;
-  a.layer = layer;
-  a.batch = batch;
-  a.max_blocks = max_blocks;
-  a.max_items = max_items;
-  __shared__ __attribute__((aligned(16))) char lds[kItemWaves * kAreaBytes];
-  __shared__ int32_t sub_tickets[kKVHeads];
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int h = w & 3;
-  const int s = w >> 2;
+__device__ __forceinline__ void load_part(const char* slot, int lane, Part& p) {
+  const int gh = (lane >> 4) & 1;
+  const float4_t a = *reinterpret_cast<const float4_t*>(slot + lane * 32);
+  const float4_t b = *reinterpret_cast<const float4_t*>(slot + lane * 32 + 16);
+  const float4_t m = *reinterpret_cast<const float4_t*>(slot + 2048 + gh * 32);
+  const float4_t l = *reinterpret_cast<const float4_t*>(slot + 2048 + gh * 32 + 16);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    p.o[0][r] = a[r];
+    p.o[1][r] = b[r];
+    p.m[r] = m[r];
+    p.l[r] = l[r];
+  }
+}
+
+// Workspace slot of part k of a cut sequence whose parts start at slot `first` (the plan
+// numbers the parts of all cut sequences densely; the last part has no slot).
+__device__ __forceinline__ char* part_slot(char* slots, int first, int k, int h) {
+  return slots + ((static_cast<int64_t>(first) + k) * kKVHeads + h) * kSlotBytes;
+}
+
+// Scalar parameters in an order whose leading ones (plan, query, pool, num_blocks, layer)
+// the compiler preloads into SGPRs at wave launch.
+__global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int32_t* plan, const _Float16* query,
+                                                                      const _Float16* pool, int64_t num_blocks,
+                                                                      int layer, int batch, int nslots, _Float16* out,
+                                                                      char* slots) {
+  __shared__ __attribute__((aligned(16))) char lds[kKVHeads * kWaveLds];
+  const int h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int c = lane & 15;
-  const int g = lane >> 4;
+  const int c = lane & 15, g = lane >> 4;
+  const int32_t* row = plan + static_cast<int64_t>(blockIdx.x) * kRowInts;
 
-  // The whole plan record in one round trip; this wave's block ids are selected from it.
-  // The empty asm makes every word (and every kernel argument the loads below need) an
-  // input before the first branch: otherwise those loads sink below the early exits, and
-  // each becomes one more dependent round trip, queued behind the K/V loads of the
-  // workgroups already running (microseconds each).
-  const int32_t* rec = a.plan + static_cast<int64_t>(blockIdx.x) * kPlanInts;
-  int32_t r[kPlanInts];
+  // The record (scalar loads) and the bin's block ids (lane L of vector k holds id 64 k + L)
+  // in one round trip: the id addresses do not depend on the record.
+  int32_t rec[kRecordInts];
 #pragma unroll
-  for (int i = 0; i < kPlanInts; ++i) r[i] = rec[i];
-  asm volatile("" ::"s"(r[0]), "s"(r[1]), "s"(r[2]), "s"(r[4]), "s"(r[5]), "s"(r[6]), "s"(r[7]), "s"(r[8]), "s"(r[9]),
-               "s"(r[10]), "s"(r[11]), "s"(r[12]), "s"(a.batch), "s"(a.max_blocks), "s"(a.max_items), "s"(a.pool),
-               "s"(a.query), "s"(a.num_blocks), "s"(a.layer));
-  const int b = r[0];
-  const int item = r[1];
-  const int len = r[2];
-  // Padding records (b < 0) and records that do not fit the call's shapes do nothing: the
-  // whole workgroup leaves before the barrier.
-  if (b < 0 || b >= a.batch || item < 0 || item >= items_of(len, a.max_blocks) || item >= a.max_items) return;
-  const int nitems = items_of(len, a.max_blocks);
-  int32_t ids[kSubBlocks];
+  for (int i = 0; i < kRecordInts; ++i) rec[i] = row[i];
+  int32_t idv[4];
 #pragma unroll
-  for (int t = 0; t < kSubBlocks; ++t) ids[t] = s == 0 ? r[4 + t] : (s == 1 ? r[4 + kSubBlocks + t] : r[4 + 2 * kSubBlocks + t]);
-  const int nblk = min(blocks_of(len), a.max_blocks);
-  const int count = min(kItemBlocks, nblk - item * kItemBlocks);  // blocks of this item, >= 1
-  const int nsub = (count + kSubBlocks - 1) / kSubBlocks;
-  const int first = item * kItemBlocks + s * kSubBlocks;          // first block of this wave
-  const int mine = min(kSubBlocks, count - s * kSubBlocks);       // its blocks (if s < nsub)
-  char* area = lds + (h * kSubs + s) * kAreaBytes;
+  for (int k = 0; k < 4; ++k) idv[k] = row[kRecordInts + 64 * k + lane];
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : "+v"(idv[0]), "+v"(idv[1]), "+v"(idv[2]), "+v"(idv[3]) :: "memory");
+  const int nseg = rec[0], nunits = rec[1];
+  if (nseg <= 0 || nseg > kMaxSegs || nunits <= 0 || nunits > kMaxUnits) return;  // padding rows do nothing
 
-  // The LDS tickets are zeroed before any wave can take one. The waves of a workgroup start
-  // together, and the record is in registers first, so no load waits behind this barrier.
-  if (w == 0 && lane < kKVHeads) sub_tickets[lane] = 0;
-  asm volatile("" ::"s"(item), "s"(len), "s"(ids[0]), "s"(ids[1]), "s"(ids[2]));
-  __syncthreads();
-  if (s >= nsub) return;
+  char* wl = lds + h * kWaveLds;
+  char* ring = wl;
+  char* qarea = wl + kRing * kUnitBytes;
+  char* oarea = qarea + kMaxSegs * 1024;
+  const int64_t kind_elems = num_blocks * kBlockElems;
+  const _Float16* lbase = pool + static_cast<int64_t>(layer) * 2 * kind_elems + h * kHeadDim;
 
-  half8_t qa, qb, k0[kSubBlocks], k1[kSubBlocks];
-  bool bad = false;
-  {
-    const int64_t kind_elems = a.num_blocks * kBlockElems;
-    const _Float16* qrow = a.query + (static_cast<int64_t>(b) * kQHeads + kGroup * h + (c & 7)) * kHeadDim + 8 * g;
-    load_pair(qa, qb, qrow);
-    const _Float16* lbase = a.pool + static_cast<int64_t>(a.layer) * 2 * kind_elems + h * kHeadDim;
-    // LDS DMA slots: instruction 0 fills rows 0..7, instruction 1 rows 8..15; lane holds the
-    // 16 B chunk stored at position lane % 8 of row lane / 8 (+ 8).
-    const int qs = lane & 7;
-    const int rA = lane >> 3, rB = rA + 8;
-    const int offA = rA * kRowElems + 8 * (2 * ((qs >> 1) ^ row_sel(rA)) + (qs & 1));
-    const int offB = rB * kRowElems + 8 * (2 * ((qs >> 1) ^ row_sel(rB)) + (qs & 1));
+  // Q of every segment into its LDS area: lane L loads q head L / 8, 16 B chunk
+  // (L % 8) ^ (L / 8). A sequence index outside the batch reads row 0 (its rows are never
+  // written).
 #pragma unroll
-    for (int t = 0; t < kSubBlocks; ++t) {
-      uint32_t id = static_cast<uint32_t>(ids[t]);
-      if (id >= static_cast<uint64_t>(a.num_blocks)) {  // negative ids wrap to huge values
-        if (t < mine) bad = true;
-        id = 0;  // never dereferenced out of the pool
-      }
-      const _Float16* kb = lbase + static_cast<int64_t>(id) * kBlockElems;
-      load_pair_stream(k0[t], k1[t], kb + c * kRowElems + 8 * g);
-      const _Float16* vb = kb + kind_elems;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + offA), lds_ptr(area + t * kHeadBlockBytes), 16, 0,
-                                       kStreamAux);
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + offB), lds_ptr(area + t * kHeadBlockBytes + 1024), 16,
-                                       0, kStreamAux);
-      __builtin_amdgcn_sched_barrier(0);  // keep the issue order the waits below count on
+  for (int s = 0; s < kMaxSegs; ++s) {
+    if (s < nseg) {
+      int b = rec[kHeaderInts + s * kSegInts];
+      b = (b < 0 || b >= batch) ? 0 : b;
+      const int qh = lane >> 3, pos = lane & 7;
+      const _Float16* src = query + (static_cast<int64_t>(b) * kQHeads + kGroup * h + qh) * kHeadDim + 8 * (pos ^ qh);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), lds_ptr(qarea + s * 1024), 16, 0, 0);
     }
   }
+  auto block_id = [&](int u) -> uint32_t {
+    const int32_t v = u < 64 ? idv[0] : u < 128 ? idv[1] : u < 192 ? idv[2] : idv[3];
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(v, u & 63));
+  };
+  // K DMA: lane L -> row L / 8 (+ 8), position L % 8 holds chunk (L % 8) ^ (row & 7).
+  const int kr = lane >> 3, kp = lane & 7;
+  const int koffA = kr * kRowElems + 8 * (kp ^ kr), koffB = (kr + 8) * kRowElems + 8 * (kp ^ kr);
+  // V DMA: lane L -> row L / 8 (+ 8), the chunk stored at position L % 8.
+  const int voffA = kr * kRowElems + 8 * (2 * ((kp >> 1) ^ row_sel(kr)) + (kp & 1));
+  const int voffB = (kr + 8) * kRowElems + 8 * (2 * ((kp >> 1) ^ row_sel(kr + 8)) + (kp & 1));
+  auto issue = [&](int u) {
+    uint32_t id = block_id(u);
+    if (id >= static_cast<uint64_t>(num_blocks)) id = 0;  // never dereferenced out of the pool
+    const _Float16* kb = lbase + static_cast<int64_t>(id) * kBlockElems;
+    const _Float16* vb = kb + kind_elems;
+    char* dst = ring + (u & (kRing - 1)) * kUnitBytes;
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(kb + koffA), lds_ptr(dst), 16, 0, kStreamAux);
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(kb + koffB), lds_ptr(dst + 1024), 16, 0, kStreamAux);
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + voffA), lds_ptr(dst + 2048), 16, 0, kStreamAux);
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + voffB), lds_ptr(dst + 3072), 16, 0, kStreamAux);
+  };
+  int issued = 0;
+  for (; issued < kRing && issued < nunits; ++issued) issue(issued);
 
+  // K reads: lane (c, g) takes row c, chunks g and 4 + g; Q reads the same chunks of row c % 8.
+  const uint32_t kaddr0 = c * 128 + ((g ^ (c & 7)) * 16), kaddr1 = c * 128 + (((4 + g) ^ (c & 7)) * 16);
+  const uint32_t qaddr0 = (c & 7) * 128 + ((g ^ (c & 7)) * 16), qaddr1 = (c & 7) * 128 + (((4 + g) ^ (c & 7)) * 16);
   // Transposing reads: lane (c, g) supplies row 4g + c/4, 8 B piece c % 4 of a dim group.
   const int rr = 4 * g + (c >> 2);
-  const uint32_t tbase = lds_offset(area) + rr * 128 + 8 * (c & 3);
   const uint32_t tsel = row_sel(rr);
+  const uint32_t ring_base = lds_offset(ring);
+
+  Part first_part, last_part;  // partials of segment 0 and of the last segment (cut sequences)
+  int seg = -1, seg_end = 0, len = 0, j0 = 0, nblk = 0, nspan = 1;
+  half8_t qa, qb;
   float m = 0.f, mc = 0.f, lsum = 0.f;
   float4_t acc[4];
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt) acc[nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  bool bad = false, first_block = true;
 
-#define PC_PROCESS_BLOCK(I)                                                                                     \
-  if (I < mine) {                                                                                               \
-    wait_loads<4 * (kSubBlocks - 1 - I)>(k0[I], k1[I]);                                                          \
-    if (I == 0) wait_loads<4 * (kSubBlocks - 1)>(qa, qb);                                                       \
-    float4_t sv = {0.f, 0.f, 0.f, 0.f};                                                                          \
-    sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0[I], qa, sv, 0, 0, 0);                                          \
-    sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1[I], qb, sv, 0, 0, 0);                                          \
-    const int valid = len - (first + I) * kSlots;                                                               \
-    float sc[4] = {sv[0], sv[1], sv[2], sv[3]};                                                                 \
-    if (valid < kSlots) {                                                                                       \
-      _Pragma("unroll") for (int q = 0; q < 4; ++q) sc[q] = 4 * g + q < valid ? sc[q] : -INFINITY;              \
-    }                                                                                                           \
-    const float bm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));                                           \
-    if (I == 0) {                                                                                               \
-      m = max_over_groups(bm); /* finite: token 0 of a wave's first block is valid */                            \
-      mc = m * kScoreToLog2;                                                                                    \
-    } else if (__builtin_amdgcn_ballot_w64(bm * kScoreToLog2 > mc + kLazyLog2) != 0) {                         \
-      const float mn = fmaxf(m, max_over_groups(bm));                                                           \
-      const float alpha = exp2_fast((m - mn) * kScoreToLog2);                                                   \
-      lsum *= alpha;                                                                                            \
-      float al[4];                                                                                              \
-      _Pragma("unroll") for (int q = 0; q < 4; ++q) al[q] = lane_value_of_half(alpha, q, (g & 1) != 0); \
-      _Pragma("unroll") for (int nt = 0; nt < 4; ++nt) _Pragma("unroll") for (int q = 0; q < 4; ++q) acc[nt][q] *= al[q]; \
-      m = mn;                                                                                                   \
-      mc = m * kScoreToLog2;                                                                                    \
-    }                                                                                                           \
-    float p[4];                                                                                                 \
-    _Pragma("unroll") for (int q = 0; q < 4; ++q) p[q] = exp2_fast(fmaf(sc[q], kScoreToLog2, -mc));             \
-    lsum += (p[0] + p[1]) + (p[2] + p[3]);                                                                      \
-    /* A operand: row c holds p of q head c % 8 for tokens 4g..4g+3: the fp16 rounding of */                    \
-    /* p for c < 8, the exact remainder scaled by 2^18 for c >= 8 */                                             \
-    half4_t pa;                                                                                                 \
-    _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                                             \
-      const float hi = static_cast<float>(static_cast<_Float16>(p[q]));                                         \
-      pa[q] = static_cast<_Float16>(c < kGroup ? p[q] : (p[q] - hi) * kLowScale);                               \
-    }                                                                                                           \
-    short4_t v0, v1, v2, v3;                                                                                    \
-    read_v_tiles<I * kHeadBlockBytes>(tbase, tsel, v0, v1, v2, v3);                                             \
-    if (valid < kSlots) {                                                                                       \
-      /* lane (c, g) holds V of tokens 4g..4g+3: zero the ones past the context */                             \
-      const int keep = valid - 4 * g;                                                                           \
-      const uint32_t mlo = (keep > 0 ? 0xFFFFu : 0u) | (keep > 1 ? 0xFFFF0000u : 0u);                           \
-      const uint32_t mhi = (keep > 2 ? 0xFFFFu : 0u) | (keep > 3 ? 0xFFFF0000u : 0u);                           \
-      uint2_t u;                                                                                                \
-      u = __builtin_bit_cast(uint2_t, v0); u[0] &= mlo; u[1] &= mhi; v0 = __builtin_bit_cast(short4_t, u);        \
-      u = __builtin_bit_cast(uint2_t, v1); u[0] &= mlo; u[1] &= mhi; v1 = __builtin_bit_cast(short4_t, u);        \
-      u = __builtin_bit_cast(uint2_t, v2); u[0] &= mlo; u[1] &= mhi; v2 = __builtin_bit_cast(short4_t, u);        \
-      u = __builtin_bit_cast(uint2_t, v3); u[0] &= mlo; u[1] &= mhi; v3 = __builtin_bit_cast(short4_t, u);        \
-    }                                                                                                           \
-    acc[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v0), acc[0], 0, 0, 0);        \
-    acc[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v1), acc[1], 0, 0, 0);        \
-    acc[2] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v2), acc[2], 0, 0, 0);        \
-    acc[3] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v3), acc[3], 0, 0, 0);        \
-  }
-
-  PC_PROCESS_BLOCK(0)
-  PC_PROCESS_BLOCK(1)
-  PC_PROCESS_BLOCK(2)
-#undef PC_PROCESS_BLOCK
-  static_assert(kSubBlocks == 3, "three PC_PROCESS_BLOCK expansions");
-  wait_all_loads(k0, k1);
-
-  // This wave's partial in the PV layout: (m, l) per q head and the folded O.
-  const float l = sum_over_groups(lsum);
-  float ox[2][4], om[4], ol[4];
+  auto finish_segment = [&]() {
+    Part p;
+    const float l = sum_over_groups(lsum);
 #pragma unroll
-  for (int k = 0; k < 2; ++k)
+    for (int k = 0; k < 2; ++k)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) ox[k][q] = bad ? NAN : fold_low_rows(acc[2 * k][q], acc[2 * k + 1][q]);
+      for (int q = 0; q < 4; ++q) p.o[k][q] = bad ? NAN : fold_low_rows(acc[2 * k][q], acc[2 * k + 1][q]);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    om[q] = lane_value_of_half(m, q, (g & 1) != 0);
-    ol[q] = lane_value_of_half(l, q, (g & 1) != 0);
-  }
-
-  Fold f;
-  if (nsub > 1) {
-    // Sub-chunk merge: every wave of kv head h leaves its partial in its own LDS area and
-    // takes a ticket; the last one folds the head's sub-chunks in order.
-    wave_lds_fence();
-    put_sub(area, lane, g, ox, om, ol);
-    int old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(&sub_tickets[h], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old != nsub - 1) return;
-    // Every sub-chunk's partial is read before the first fold (one LDS round trip; the
-    // area of a sub-chunk past nsub is read and not folded).
-    float px[kSubs][2][4], pm[kSubs][4], pl[kSubs][4];
-#pragma unroll
-    for (int s2 = 0; s2 < kSubs; ++s2) get_sub(lds + (h * kSubs + s2) * kAreaBytes, lane, g, px[s2], pm[s2], pl[s2]);
-    f.set(pm[0], pl[0], px[0]);
-#pragma unroll
-    for (int s2 = 1; s2 < kSubs; ++s2) {
-      if (s2 < nsub) f.add(pm[s2], pl[s2], px[s2]);
+    for (int q = 0; q < 4; ++q) {
+      p.m[q] = lane_value_of_half(m, q, (g & 1) != 0);
+      p.l[q] = lane_value_of_half(l, q, (g & 1) != 0);
     }
-  } else {
-    f.set(om, ol, ox);
-  }
-
-  if (nitems == 1) {
-    float inv[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) inv[q] = 1.0f / f.L[q];
-    store_natural<true>(a.out + (static_cast<int64_t>(b) * kQHeads + kGroup * h) * kHeadDim, area, lane, f.O, inv);
-    return;
-  }
-  float* part = a.partials + ((static_cast<int64_t>(b) * kKVHeads + h) * a.max_items + item) * kPartFloats;
-  store_natural<false>(part, area, lane, f.O, f.L);
-  if (lane == 0 || lane == 16) {
-    *reinterpret_cast<float4_t*>(part + 512 + (g & 1) * 8) = float4_t{f.M[0], f.L[0], f.M[1], f.L[1]};
-    *reinterpret_cast<float4_t*>(part + 512 + (g & 1) * 8 + 4) = float4_t{f.M[2], f.L[2], f.M[3], f.L[3]};
-  }
-}
-
-// Merge of multi-item sequences: one workgroup per (sequence, kv head); thread t owns dims
-// 2(t % 32), +1 of q head t / 32 and folds the items' partials in item order, the loads of
-// up to kMergeItems items issued at once.
-__global__ __launch_bounds__(kMergeThreads) void paged_decode_merge_kernel(const int32_t* context_lens, int max_blocks,
-                                                                         int max_items, const float* partials,
-                                                                         _Float16* out) {
-  AttnArgs a;
-  a.out = out;
-  a.context_lens = context_lens;
-  a.partials = const_cast<float*>(partials);
-  a.max_blocks = max_blocks;
-  a.max_items = max_items;
-  const int grp = blockIdx.x;
-  const int b = grp / kKVHeads, h = grp % kKVHeads;
-  const int t = threadIdx.x;
-  const int qh = t >> 5;
-  const int d = 2 * (t & 31);
-  const int nitems = min(items_of(a.context_lens[b], a.max_blocks), a.max_items);
-  if (nitems <= 1) return;
-  const float* gpart = a.partials + static_cast<int64_t>(grp) * a.max_items * kPartFloats;
-  float M = -INFINITY, L = 0.f, O0 = 0.f, O1 = 0.f;
-#pragma unroll 1
-  for (int i0 = 0; i0 < nitems; i0 += kMergeItems) {
-    float2_t x[kMergeItems], ml[kMergeItems];
-#pragma unroll
-    for (int i = 0; i < kMergeItems; ++i) {
-      const float* p = gpart + static_cast<int64_t>(min(i0 + i, nitems - 1)) * kPartFloats;  // clamped: in bounds
-      x[i] = *reinterpret_cast<const float2_t*>(p + qh * kHeadDim + d);
-      ml[i] = *reinterpret_cast<const float2_t*>(p + 512 + 2 * qh);
+    if (nspan == 1) {
+      wave_lds_fence();
+      put_output(oarea + seg * 1024, lane, p);
+    } else {
+      if (seg == 0) first_part = p;
+      if (seg == nseg - 1) last_part = p;
     }
+  };
+
+  for (int u = 0; u < nunits; ++u) {
+    if (u == seg_end) {
+      if (seg >= 0) finish_segment();
+      if (++seg >= nseg) break;  // malformed record: blocks beyond the segments are not processed
+      len = seg == 0 ? rec[9] : seg == 1 ? rec[17] : seg == 2 ? rec[25] : rec[33];
+      j0 = seg == 0 ? rec[10] : seg == 1 ? rec[18] : seg == 2 ? rec[26] : rec[34];
+      nblk = seg == 0 ? rec[11] : seg == 1 ? rec[19] : seg == 2 ? rec[27] : rec[35];
+      nspan = seg == 0 ? rec[14] : seg == 1 ? rec[22] : seg == 2 ? rec[30] : rec[38];
+      seg_end = u + max(nblk, 1);
+      bad = false;
+      first_block = true;
+      lsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMergeItems; ++i) {
-      // Branch-free: a clamped duplicate gets weight 0 (m stays finite from the first item).
-      const bool used = i0 + i < nitems;
-      const float mp = used ? ml[i][0] : -INFINITY;
-      const float lp = used ? ml[i][1] : 0.f;
-      const float mn = fmaxf(M, mp);
-      const float so = exp2_fast((M - mn) * kScoreToLog2);
-      const float sn = exp2_fast((mp - mn) * kScoreToLog2);
-      L = fmaf(lp, sn, L * so);
-      O0 = fmaf(used ? x[i][0] : 0.f, sn, O0 * so);
-      O1 = fmaf(used ? x[i][1] : 0.f, sn, O1 * so);
-      M = mn;
+      for (int nt = 0; nt < 4; ++nt) acc[nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    wait_ring(issued - u - 1);  // also covers the Q DMAs, issued before every unit
+    if (first_block) {
+      const uint32_t qbase = lds_offset(qarea + seg * 1024);
+      asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                   : "=&v"(qa), "=&v"(qb)
+                   : "v"(qbase + qaddr0), "v"(qbase + qaddr1)
+                   : "memory");
+    }
+    if (block_id(u) >= static_cast<uint64_t>(num_blocks)) bad = true;
+    const uint32_t slot = ring_base + (u & (kRing - 1)) * kUnitBytes;
+    half8_t k0v, k1v;
+    short4_t v0, v1, v2, v3;
+    {
+      const uint32_t vbase = slot + rr * 128 + 8 * (c & 3);
+      asm volatile(
+          "ds_read_b128 %0, %6\n\t"
+          "ds_read_b128 %1, %7\n\t"
+          "ds_read_b64_tr_b16 %2, %8 offset:2048\n\t"
+          "ds_read_b64_tr_b16 %3, %9 offset:2048\n\t"
+          "ds_read_b64_tr_b16 %4, %10 offset:2048\n\t"
+          "ds_read_b64_tr_b16 %5, %11 offset:2048\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(k0v), "=&v"(k1v), "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+          : "v"(slot + kaddr0), "v"(slot + kaddr1), "v"(vbase + 32 * (0 ^ tsel)), "v"(vbase + 32 * (1 ^ tsel)),
+            "v"(vbase + 32 * (2 ^ tsel)), "v"(vbase + 32 * (3 ^ tsel))
+          : "memory");
+    }
+    // The slot's LDS reads are complete: refill it with the unit kRing ahead.
+    if (issued < nunits) {
+      issue(issued);
+      ++issued;
+    }
+    float4_t sv = {0.f, 0.f, 0.f, 0.f};
+    sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0v, qa, sv, 0, 0, 0);
+    sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1v, qb, sv, 0, 0, 0);
+    const int valid = len - (j0 + (u - (seg_end - nblk))) * kSlots;
+    float sc[4] = {sv[0], sv[1], sv[2], sv[3]};
+    if (valid < kSlots) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sc[q] = 4 * g + q < valid ? sc[q] : -INFINITY;
+    }
+    const float bm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    if (first_block) {
+      m = max_over_groups(bm);  // finite: token 0 of a segment's first block is valid
+      mc = m * kScoreToLog2;
+      first_block = false;
+    } else if (__builtin_amdgcn_ballot_w64(bm * kScoreToLog2 > mc + kLazyLog2) != 0) {
+      const float mn = fmaxf(m, max_over_groups(bm));
+      const float alpha = exp2_fast((m - mn) * kScoreToLog2);
+      lsum *= alpha;
+      float al[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) al[q] = lane_value_of_half(alpha, q, (g & 1) != 0);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[nt][q] *= al[q];
+      m = mn;
+      mc = m * kScoreToLog2;
+    }
+    float p[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) p[q] = exp2_fast(fmaf(sc[q], kScoreToLog2, -mc));
+    lsum += (p[0] + p[1]) + (p[2] + p[3]);
+    // A operand: row c holds p of q head c % 8 for tokens 4g..4g+3: the fp16 rounding of p
+    // for c < 8, the exact remainder scaled by 2^18 for c >= 8.
+    half4_t pa;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float hi = static_cast<float>(static_cast<_Float16>(p[q]));
+      pa[q] = static_cast<_Float16>(c < kGroup ? p[q] : (p[q] - hi) * kLowScale);
+    }
+    if (valid < kSlots) {
+      // lane (c, g) holds V of tokens 4g..4g+3: zero the ones past the context
+      const int keep = valid - 4 * g;
+      const uint32_t mlo = (keep > 0 ? 0xFFFFu : 0u) | (keep > 1 ? 0xFFFF0000u : 0u);
+      const uint32_t mhi = (keep > 2 ? 0xFFFFu : 0u) | (keep > 3 ? 0xFFFF0000u : 0u);
+      uint2_t x;
+      x = __builtin_bit_cast(uint2_t, v0); x[0] &= mlo; x[1] &= mhi; v0 = __builtin_bit_cast(short4_t, x);
+      x = __builtin_bit_cast(uint2_t, v1); x[0] &= mlo; x[1] &= mhi; v1 = __builtin_bit_cast(short4_t, x);
+      x = __builtin_bit_cast(uint2_t, v2); x[0] &= mlo; x[1] &= mhi; v2 = __builtin_bit_cast(short4_t, x);
+      x = __builtin_bit_cast(uint2_t, v3); x[0] &= mlo; x[1] &= mhi; v3 = __builtin_bit_cast(short4_t, x);
+    }
+    acc[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v0), acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v1), acc[1], 0, 0, 0);
+    acc[2] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v2), acc[2], 0, 0, 0);
+    acc[3] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, v3), acc[3], 0, 0, 0);
+  }
+  if (seg < nseg) finish_segment();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every DMA has landed (also after a malformed record)
+  const bool complete = seg == nseg - 1 && seg_end == nunits;  // the record's segments cover its blocks
+
+  // Segment fields of the first and the last segment.
+  const int b0 = rec[8], k00 = rec[12], kidx0 = rec[13], nspan0 = rec[14], slot0 = rec[15];
+  const int sl = nseg - 1;
+  const int kidxl = sl == 0 ? rec[13] : sl == 1 ? rec[21] : sl == 2 ? rec[29] : rec[37];
+  const int nspanl = sl == 0 ? rec[14] : sl == 1 ? rec[22] : sl == 2 ? rec[30] : rec[38];
+  const int slotl = sl == 0 ? rec[15] : sl == 1 ? rec[23] : sl == 2 ? rec[31] : rec[39];
+  // The span's slots [first, first + parts - 1) lie in the workspace.
+  auto slots_ok = [&](int first, int parts) { return first >= 0 && parts >= 2 && first + static_cast<int64_t>(parts) - 1 <= nslots; };
+
+  // A part that is not the last of its span: store it, wait for the acknowledgement, then
+  // raise the part's flag (the writer's XCD id + 1 in bits 8..15, 1 in bits 0..7).
+  if (complete && nspanl > 1 && kidxl < nspanl - 1 && kidxl >= 0 && slots_ok(slotl, nspanl)) {
+    char* slot = part_slot(slots, slotl, kidxl, h);
+    store_part(slot, lane, last_part);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0) {
+      __hip_atomic_store(reinterpret_cast<int32_t*>(slot + kFlagOffset), 1 + ((xcc_id() + 1) << 8), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  const float inv = 1.0f / L;
-  *reinterpret_cast<half2_t*>(a.out + (static_cast<int64_t>(b) * kQHeads + kGroup * h + qh) * kHeadDim + d) =
-      half2_t{static_cast<_Float16>(O0 * inv), static_cast<_Float16>(O1 * inv)};
+  // Sequences complete within the bin: their fp16 rows from LDS.
+  wave_lds_fence();
+#pragma unroll
+  for (int s = 0; s < kMaxSegs; ++s) {
+    const int sb = rec[kHeaderInts + s * kSegInts];
+    if (complete && s < nseg && rec[kHeaderInts + s * kSegInts + 6] == 1 && sb >= 0 && sb < batch) {
+      *reinterpret_cast<uint4*>(out + (static_cast<int64_t>(sb) * kQHeads + kGroup * h) * kHeadDim + lane * 8) =
+          *reinterpret_cast<const uint4*>(oarea + s * 1024 + lane * 16);
+    }
+  }
+  // The last part of a cut sequence: wait for the other parts' flags, fold them in span
+  // order and this bin's part last, write the rows, lower the flags.
+  if (complete && nspan0 > 1 && kidx0 == nspan0 - 1 && slots_ok(slot0, nspan0) &&
+      k00 + static_cast<int64_t>(kGroups) * kidx0 == static_cast<int64_t>(blockIdx.x) && k00 >= 0) {
+    const int want = 1 + ((xcc_id() + 1) << 8);
+    bool ok = true;
+    for (int k = 0; k < nspan0 - 1; ++k) {
+      const int32_t* flag = reinterpret_cast<const int32_t*>(part_slot(slots, slot0, k, h) + kFlagOffset);
+      int f = 0;
+      for (int spins = 0; spins < kMaxSpins; ++spins) {
+        f = sload_glc(flag);
+        if (f != 0) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (f != want) ok = false;  // never raised, or raised on another XCD (its partial is not visible here)
+    }
+    Part acc_p;
+    for (int k0s = 0; k0s < nspan0 - 1; k0s += 8) {
+      Part pp[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) load_part(part_slot(slots, slot0, min(k0s + i, nspan0 - 2), h), lane, pp[i]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (k0s + i >= nspan0 - 1) break;
+        if (k0s + i == 0) acc_p = pp[i]; else fold_part(acc_p, pp[i]);
+      }
+    }
+    fold_part(acc_p, first_part);
+    if (!ok) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        acc_p.o[0][r] = NAN;
+        acc_p.o[1][r] = NAN;
+      }
+    }
+    if (b0 >= 0 && b0 < batch) {
+      wave_lds_fence();
+      put_output(ring, lane, acc_p);  // the ring is free after the stream
+      wave_lds_fence();
+      *reinterpret_cast<uint4*>(out + (static_cast<int64_t>(b0) * kQHeads + kGroup * h) * kHeadDim + lane * 8) =
+          *reinterpret_cast<const uint4*>(ring + lane * 16);
+    }
+    for (int k = lane; k < nspan0 - 1; k += 64) {
+      __hip_atomic_store(reinterpret_cast<int32_t*>(part_slot(slots, slot0, k, h) + kFlagOffset), 0, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------
 // Host-side validation, plan and workspace layout.
 // ---------------------------------------------------------------------------------------
 
-int64_t items_per_sequence(int32_t max_blocks) { return (static_cast<int64_t>(max_blocks) + kItemBlocks - 1) / kItemBlocks; }
-
 int check_attn_shape(int32_t batch, int32_t max_blocks) {
   if (batch < 0 || batch > (1 << 20)) return set_error(PC_ERR_ARGUMENT, "batch %d out of range", batch);
   if (max_blocks < 1 || max_blocks > (1 << 16)) {
     return set_error(PC_ERR_ARGUMENT, "max_blocks %d out of range [1, 65536]", max_blocks);
   }
-  if ((static_cast<int64_t>(batch) + kPlanBins) * items_per_sequence(max_blocks) > INT32_MAX) {
-    return set_error(PC_ERR_ARGUMENT, "attention grid too large");
-  }
   return PC_OK;
 }
+
+// Bins of one group the planner may create for a batch of `batch` sequences of at most
+// `max_blocks` blocks: the nominal cut (at most the whole target, or one bin per kMaxUnits
+// blocks when that is more), plus one early close per kMaxSegs - 1 complete sequences (a bin
+// closed at kMaxSegs segments holds at least that many), plus one.
+int64_t group_bins_bound(int32_t batch, int32_t max_blocks) {
+  const int64_t total = static_cast<int64_t>(batch) * max_blocks;
+  const int64_t nominal = std::max<int64_t>(kTargetBins, (total + kMaxUnits - 1) / kMaxUnits);
+  return nominal + 1 + (batch + kMaxSegs - 2) / (kMaxSegs - 1) + 1;
+}
+
+// Plan rows (workgroups) that always suffice for the shape.
+int64_t plan_rows_bound(int32_t batch, int32_t max_blocks) {
+  return static_cast<int64_t>(kGroups) * group_bins_bound(batch, max_blocks);
+}
+
+// Partial slots that always suffice: one per bin at most (a bin ends at most one cut part
+// that is not a sequence's last). The bins over all groups number at most the target plus
+// one per kMaxUnits blocks plus rounding (kGroups x 1.5), plus the early closes.
+int64_t slots_bound(int32_t batch, int32_t max_blocks) {
+  const int64_t total = static_cast<int64_t>(batch) * max_blocks;
+  return kTargetBins + (total + kMaxUnits - 1) / kMaxUnits + 2 * kGroups + (batch + kMaxSegs - 2) / (kMaxSegs - 1);
+}
+
+int64_t workspace_bytes_for(int64_t slots) { return slots * kKVHeads * kSlotBytes; }
 
 // Split-K scratch of pc_paged_decode_attn_noalloc: a file-scope device array, one copy per
 // GPU, held until the process ends. Host code never passes `scratch` itself to a kernel (in
 // host code the name is a stand-in, not a device address); it uses the address
-// hipGetSymbolAddress returns for the device, looked up once per device.
+// hipGetSymbolAddress returns for the device, looked up once per device. Its contents start
+// at zero (part flags must) and every call leaves them so.
 constexpr int64_t kNoAllocScratchBytes = PC_ATTN_NOALLOC_SCRATCH_BYTES;
 static_assert(kNoAllocScratchBytes % 256 == 0, "the scratch keeps the workspace's 256-byte alignment");
 __device__ __align__(256) char scratch[kNoAllocScratchBytes];
@@ -671,6 +714,13 @@ void* scratch_address(int device) {
   return g_scratch_ptr[device];
 }
 
+// One bin while it is being cut: its segments {sequence, first block, blocks}.
+struct BinSegs {
+  int32_t seg[kMaxSegs][3];
+  int nseg = 0;
+  int blocks = 0;
+};
+
 }  // namespace
 
 extern "C" {
@@ -679,72 +729,146 @@ int pc_abi_version(void) { return kAbiVersion; }
 
 const char* pc_last_error(void) { return pc_internal::last_error(); }
 
-int32_t pc_attn_plan_record_ints(void) { return kPlanInts; }
+int32_t pc_attn_plan_record_ints(void) { return kRowInts; }
 
 int64_t pc_attn_plan_capacity(int32_t batch, int32_t max_blocks) {
   if (check_attn_shape(batch, max_blocks) != PC_OK) return -1;
-  // Greedy binning leaves no bin more than one sequence's items above the average.
-  return (static_cast<int64_t>(batch) + kPlanBins) * items_per_sequence(max_blocks);
+  return plan_rows_bound(batch, max_blocks);
 }
 
 int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks) {
   if (check_attn_shape(batch, max_blocks) != PC_OK) return 0;
-  return static_cast<int64_t>(batch) * kKVHeads * items_per_sequence(max_blocks) * kPartFloats * 4;
+  return workspace_bytes_for(slots_bound(batch, max_blocks));
 }
 
 int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, int32_t batch, int32_t max_blocks,
                      int32_t* plan, int64_t capacity) {
   if (int rc = check_attn_shape(batch, max_blocks)) return -rc;
   if (batch > 0 && (!context_lens || !block_tables || !plan)) return -set_error(PC_ERR_ARGUMENT, "null pointer");
-  // Sequences, longest first, go to the bin (XCD) with the fewest items so far; work item k
-  // of bin x becomes record k * kPlanBins + x, and the hardware dispatches workgroup i to XCD
-  // (i + start) % 8, so the items of one sequence share an XCD and its L2. Bins shorter than
-  // the longest are padded with empty records.
   std::vector<int32_t> order;
   order.reserve(batch);
+  int64_t total = 0;
   for (int32_t b = 0; b < batch; ++b) {
     if (context_lens[b] > static_cast<int64_t>(max_blocks) * kSlots) {
       return -set_error(PC_ERR_ARGUMENT, "context length %d of sequence %d exceeds its %d-block table", context_lens[b], b,
                         max_blocks);
     }
-    if (context_lens[b] > 0) order.push_back(b);
-  }
-  std::stable_sort(order.begin(), order.end(), [&](int32_t x, int32_t y) { return context_lens[x] > context_lens[y]; });
-  std::vector<std::vector<int32_t>> bins(kPlanBins);
-  std::vector<int64_t> load(kPlanBins, 0);
-  for (int32_t b : order) {
-    const int32_t len = context_lens[b];
-    const int32_t nblk = blocks_of(len);  // <= max_blocks, checked above
-    const int32_t nitems = (nblk + kItemBlocks - 1) / kItemBlocks;
-    const int bin = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
-    load[bin] += nitems;
-    const int32_t* row = block_tables + static_cast<int64_t>(b) * max_blocks;
-    for (int32_t item = 0; item < nitems; ++item) {
-      int32_t rec[kPlanInts] = {b, item, len, nitems};
-      for (int i = 0; i < kItemBlocks; ++i) rec[4 + i] = row[std::min(item * kItemBlocks + i, nblk - 1)];
-      bins[bin].insert(bins[bin].end(), rec, rec + kPlanInts);
+    if (context_lens[b] > 0) {
+      order.push_back(b);
+      total += blocks_of(context_lens[b]);
     }
   }
-  int64_t most = 0;
-  for (const auto& v : bins) most = std::max<int64_t>(most, static_cast<int64_t>(v.size()) / kPlanInts);
-  const int64_t total = most * kPlanBins;
-  if (total > capacity) {
-    return -set_error(PC_ERR_ARGUMENT, "plan capacity %lld too small (%lld records)", static_cast<long long>(capacity),
-                      static_cast<long long>(total));
+  if (total == 0) return (ok(), 0);
+  // Sequences, longest first, go to the group with the fewest blocks so far.
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int32_t x, int32_t y) { return blocks_of(context_lens[x]) > blocks_of(context_lens[y]); });
+  std::vector<std::vector<int32_t>> members(kGroups);
+  std::vector<int64_t> load(kGroups, 0);
+  for (int32_t b : order) {
+    const int x = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
+    members[x].push_back(b);
+    load[x] += blocks_of(context_lens[b]);
   }
-  for (int64_t pos = 0; pos < most; ++pos) {
-    for (int x = 0; x < kPlanBins; ++x) {
-      int32_t* dst = plan + (pos * kPlanBins + x) * kPlanInts;
-      if (pos < static_cast<int64_t>(bins[x].size()) / kPlanInts) {
-        std::copy(bins[x].begin() + pos * kPlanInts, bins[x].begin() + (pos + 1) * kPlanInts, dst);
-      } else {
-        std::fill(dst, dst + kPlanInts, 0);
-        dst[0] = -1;
+  // Bins over the whole batch: one per CU, fewer for small workloads, more when a bin would
+  // exceed kMaxUnits blocks; each group gets its share, cut at equal block counts.
+  const int64_t target = std::max<int64_t>(std::min<int64_t>(kTargetBins, std::max<int64_t>(1, total / kMinBinBlocks)),
+                                           (total + kMaxUnits - 1) / kMaxUnits);
+  std::vector<std::vector<BinSegs>> bins(kGroups);
+  for (int x = 0; x < kGroups; ++x) {
+    if (load[x] == 0) continue;
+    int64_t nb = (target * load[x] + total / 2) / total;
+    nb = std::max<int64_t>(nb, (load[x] + kMaxUnits - 1) / kMaxUnits);
+    nb = std::max<int64_t>(1, std::min<int64_t>(nb, load[x]));
+    // Bin i nominally ends at block floor((i + 1) load / nb) of the group; a bin also closes
+    // when it holds kMaxSegs segments and the next block starts another sequence.
+    auto boundary_after = [&](int64_t pos) {
+      const int64_t i = (pos * nb) / load[x];  // first i with (i + 1) load / nb > pos
+      for (int64_t j = std::max<int64_t>(0, i - 1);; ++j) {
+        const int64_t e = ((j + 1) * load[x]) / nb;
+        if (e > pos) return e;
+      }
+    };
+    std::vector<BinSegs>& out = bins[x];
+    BinSegs cur;
+    int64_t pos = 0, end = boundary_after(0);
+    for (int32_t b : members[x]) {
+      const int32_t n = blocks_of(context_lens[b]);
+      int32_t j = 0;
+      while (j < n) {
+        if (cur.blocks > 0 && (pos == end || cur.nseg == kMaxSegs)) {
+          out.push_back(cur);
+          cur = BinSegs();
+          end = boundary_after(pos);
+        }
+        const int32_t take = static_cast<int32_t>(std::min<int64_t>(n - j, end - pos));
+        cur.seg[cur.nseg][0] = b;
+        cur.seg[cur.nseg][1] = j;
+        cur.seg[cur.nseg][2] = take;
+        ++cur.nseg;
+        cur.blocks += take;
+        j += take;
+        pos += take;
+      }
+    }
+    if (cur.blocks > 0) out.push_back(cur);
+  }
+  size_t most = 0;
+  for (const auto& v : bins) most = std::max(most, v.size());
+  const int64_t rows = static_cast<int64_t>(most) * kGroups;
+  if (rows > capacity || rows > INT32_MAX) {
+    return -set_error(PC_ERR_ARGUMENT, "plan capacity %lld too small (%lld rows)", static_cast<long long>(capacity),
+                      static_cast<long long>(rows));
+  }
+  // Each sequence's bins (rows), in order, and the first slot of each cut sequence.
+  std::vector<int32_t> first_row(batch, -1), nspan(batch, 0), first_slot(batch, -1);
+  for (int x = 0; x < kGroups; ++x) {
+    for (size_t i = 0; i < bins[x].size(); ++i) {
+      const BinSegs& bs = bins[x][i];
+      for (int s = 0; s < bs.nseg; ++s) {
+        const int32_t b = bs.seg[s][0];
+        if (first_row[b] < 0) first_row[b] = static_cast<int32_t>(x + kGroups * i);
+        ++nspan[b];
+      }
+    }
+  }
+  int64_t slots = 0;
+  for (int32_t b = 0; b < batch; ++b) {
+    if (nspan[b] > 1) {
+      first_slot[b] = static_cast<int32_t>(slots);
+      slots += nspan[b] - 1;
+    }
+  }
+  if (slots > slots_bound(batch, max_blocks)) {
+    return -set_error(PC_ERR_ARGUMENT, "plan needs %lld partial slots, above the workspace's %lld",
+                      static_cast<long long>(slots), static_cast<long long>(slots_bound(batch, max_blocks)));
+  }
+  std::fill(plan, plan + rows * kRowInts, 0);
+  for (int x = 0; x < kGroups; ++x) {
+    for (size_t i = 0; i < bins[x].size(); ++i) {
+      const BinSegs& bs = bins[x][i];
+      const int32_t r = static_cast<int32_t>(x + kGroups * i);
+      int32_t* row = plan + static_cast<int64_t>(r) * kRowInts;
+      row[0] = bs.nseg;
+      row[1] = bs.blocks;
+      int u = 0;
+      for (int s = 0; s < bs.nseg; ++s) {
+        const int32_t b = bs.seg[s][0], j0 = bs.seg[s][1], n = bs.seg[s][2];
+        int32_t* seg = row + kHeaderInts + s * kSegInts;
+        seg[0] = b;
+        seg[1] = context_lens[b];
+        seg[2] = j0;
+        seg[3] = n;
+        seg[4] = first_row[b];
+        seg[5] = (r - first_row[b]) / kGroups;
+        seg[6] = nspan[b];
+        seg[7] = first_slot[b];
+        const int32_t* table = block_tables + static_cast<int64_t>(b) * max_blocks;
+        for (int32_t j = 0; j < n; ++j) row[kRecordInts + u++] = table[j0 + j];
       }
     }
   }
   ok();
-  return static_cast<int32_t>(total);
+  return static_cast<int32_t>(rows);
 }
 
 int pc_kv_append(void* pool, int64_t num_blocks, int32_t layer_begin, int32_t num_layers,
@@ -797,42 +921,25 @@ int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t
                          const int32_t* context_lens, int32_t batch, int32_t max_blocks, const int32_t* plan,
                          int32_t num_records, void* workspace, void* stream) {
   if (!out || !query || !pool || !context_lens || !plan) return set_error(PC_ERR_ARGUMENT, "null pointer");
+  if (!workspace) return set_error(PC_ERR_ARGUMENT, "workspace required (null pointer)");
   if (num_blocks < 1 || num_blocks > INT32_MAX) return set_error(PC_ERR_ARGUMENT, "num_blocks out of range");
   if (layer < 0 || layer >= kLayers) return set_error(PC_ERR_ARGUMENT, "layer %d outside [0, 22)", layer);
   if (int rc = check_attn_shape(batch, max_blocks)) return rc;
-  const int64_t max_items = items_per_sequence(max_blocks);
-  if (max_items > 1 && !workspace) return set_error(PC_ERR_ARGUMENT, "workspace required");
   if (!aligned(query, 16) || !aligned(out, 16) || !aligned(pool, 16) || !aligned(workspace, 256) ||
       !aligned(plan, 16) || !aligned(context_lens, 4)) {
     return set_error(PC_ERR_ARGUMENT, "query/out/pool/plan must be 16-byte, workspace 256-byte aligned");
   }
-  if (num_records < 0 || num_records > (static_cast<int64_t>(batch) + kPlanBins) * max_items) {
-    return set_error(PC_ERR_ARGUMENT, "num_records %d outside [0, (batch + 8) * items per sequence]", num_records);
+  if (num_records < 0 || num_records > plan_rows_bound(batch, max_blocks)) {
+    return set_error(PC_ERR_ARGUMENT, "num_records %d outside [0, pc_attn_plan_capacity]", num_records);
   }
+  const int64_t nslots = slots_bound(batch, max_blocks);
   if (batch == 0 || num_records == 0) return ok();
-  AttnArgs a;
-  a.out = static_cast<_Float16*>(out);
-  a.query = static_cast<const _Float16*>(query);
-  a.pool = static_cast<const _Float16*>(pool);
-  a.num_blocks = num_blocks;
-  a.plan = plan;
-  a.context_lens = context_lens;
-  a.partials = static_cast<float*>(workspace);
-  a.layer = layer;
-  a.batch = batch;
-  a.max_blocks = max_blocks;
-  a.max_items = static_cast<int>(max_items);
   hipStream_t s = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
-  hipLaunchKernelGGL(paged_decode_item_kernel, dim3(static_cast<unsigned>(num_records)), dim3(kItemThreads), 0, s, a.plan,
-                     a.query, a.pool, a.num_blocks, a.layer, a.batch, a.max_blocks, a.max_items, a.out, a.partials);
-  if (int rc = check_launch("paged_decode_item")) return rc;
-  if (max_items > 1) {
-    hipLaunchKernelGGL(paged_decode_merge_kernel, dim3(static_cast<unsigned>(batch) * kKVHeads), dim3(kMergeThreads), 0,
-                       s, a.context_lens, a.max_blocks, a.max_items, static_cast<const float*>(a.partials), a.out);
-    return check_launch("paged_decode_merge");
-  }
-  return PC_OK;
+  hipLaunchKernelGGL(paged_decode_bin_kernel, dim3(static_cast<unsigned>(num_records)), dim3(kBinThreads), 0, s, plan,
+                     static_cast<const _Float16*>(query), static_cast<const _Float16*>(pool), num_blocks, layer, batch,
+                     static_cast<int>(nslots), static_cast<_Float16*>(out), static_cast<char*>(workspace));
+  return check_launch("paged_decode_bin");
 }
 
 int pc_paged_decode_attn_noalloc(void* out, const void* query, const void* pool, int64_t num_blocks, int32_t layer,
@@ -840,7 +947,7 @@ int pc_paged_decode_attn_noalloc(void* out, const void* query, const void* pool,
                                  int32_t num_records, void* stream) {
   // The size check comes first: a call beyond the scratch is refused before any HIP call.
   if (int rc = check_attn_shape(batch, max_blocks)) return rc;
-  const int64_t need = static_cast<int64_t>(batch) * kKVHeads * items_per_sequence(max_blocks) * kPartFloats * 4;
+  const int64_t need = workspace_bytes_for(slots_bound(batch, max_blocks));
   if (need > kNoAllocScratchBytes) {
     return set_error(PC_ERR_ARGUMENT,
                      "batch %d with %d-block tables needs %lld bytes of split-K scratch; the allocation-free entry "

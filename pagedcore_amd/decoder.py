@@ -360,10 +360,12 @@ class DecodeGraph:
     cost more host time than the GPU needs to run them. Here the step's device work is
     captured once, with every per-step input in static device buffers: token ids, the
     staged token's slot and position of each row, the staged context lengths, and the
-    decode plan at its full capacity (pc_attn_plan_capacity records for the batch and
-    128-block tables, the tail padded with empty records). Per step the host does the
-    allocator's staged-append bookkeeping, builds the plan into a pinned buffer, uploads
-    it with two asynchronous copies and replays the graph; nothing synchronizes.
+    decode plan at its full capacity (pc_attn_plan_capacity rows for the batch and
+    128-block tables; the attention kernel launches one workgroup per row and empty rows
+    exit at once). Per step the host does the allocator's staged-append bookkeeping, builds
+    the plan into a pinned buffer, uploads the rows in use (and the empty rows that replace
+    a longer previous plan) with two asynchronous copies and replays the graph; nothing
+    synchronizes.
 
     Same checks, errors and staged-append semantics as decode_paged for any 1 to `batch`
     requests (any requests, in any order, step to step). A batch of exactly `batch`
@@ -396,8 +398,8 @@ class DecodeGraph:
         self._inputs32 = torch.zeros(self._lens_span + self._capacity * fields, dtype=torch.int32, device=device)
         self._lens = self._inputs32[:batch]
         self._plan = self._inputs32[self._lens_span :].view(self._capacity, fields)
-        self._plan[:, 0] = -1
-        self._workspace = torch.empty(max(256, _hip.workspace_bytes(batch, MAX_BLOCKS)), dtype=torch.uint8, device=device)
+        self._fields = fields
+        self._workspace = torch.zeros(max(256, _hip.workspace_bytes(batch, MAX_BLOCKS)), dtype=torch.uint8, device=device)
         # Two pinned staging buffers used in turn; an event marks when a buffer's upload
         # has run, so it is not refilled while its copy may still be pending.
         self._host = [
@@ -408,6 +410,8 @@ class DecodeGraph:
             for _ in range(2)
         ]
         self._uploaded: list = [None, None]
+        self._host_rows = [0, 0]  # plan rows a pinned buffer may hold non-empty
+        self._device_rows = 0  # plan rows the device buffer may hold non-empty
         self._turn = 0
 
         stream = torch.cuda.current_stream(device)
@@ -476,9 +480,14 @@ class DecodeGraph:
             h64[2, rows:] = 0
             h32[:rows] = staged.lengths
             h32[rows : self.batch] = 0
-            _hip.decode_plan_into(staged.lengths, staged.tables, h32[self._lens_span :].reshape(self._capacity, -1))
+            count = _hip.decode_plan_into(
+                staged.lengths, staged.tables, h32[self._lens_span :].reshape(self._capacity, -1), self._host_rows[turn]
+            )
+            self._host_rows[turn] = count
+            upload = self._lens_span + max(count, self._device_rows) * self._fields
+            self._device_rows = count
             self._inputs64[1:].copy_(host64[1:], non_blocking=True)
-            self._inputs32.copy_(host32, non_blocking=True)
+            self._inputs32[:upload].copy_(host32[:upload], non_blocking=True)
             uploaded = torch.cuda.Event()
             uploaded.record()
             self._uploaded[turn] = uploaded

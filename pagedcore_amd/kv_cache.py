@@ -708,7 +708,7 @@ class KVAllocator:
         return batch.tables, batch.lengths
 
     def decode_plan(self, request_ids: Sequence[RequestId], *, layer_index: int) -> Tensor:
-        """Device decode plan (pc_attn_plan records: row, item, length, block ids) for the
+        """Device decode plan (pc_attn_plan rows: balanced bins of the batch's blocks) for the
         batch that gather_block_tables returns, built once per allocator state from the host
         tables, so the 22 layers of a decode step share it."""
         batch = self._gather(request_ids, layer_index)

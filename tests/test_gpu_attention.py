@@ -21,6 +21,7 @@ import torch
 from oracle import paged_reference as ref
 from pagedcore_amd import _hip
 from tests import workloads
+from tests.bin_plan import check_decode_plan, regrouped_plan
 from pagedcore_amd.attention import paged_attention, paged_attention_batch
 from pagedcore_amd.engine_types import CapacityCounts, KVReservation, RequestId
 from pagedcore_amd.kv_cache import KVAllocator
@@ -279,18 +280,18 @@ def _oracle_rows(pool, layer, w, queries, rows):
 
 
 def _shuffled_plan(w, seed):
-    """The decode plan with its records (padding included) in a random order: the dispatch
-    order, and so the XCD each item runs on, changes; the answer must not."""
+    """The decode plan with its 8 groups of bins moved to other groups in a random order:
+    every bin runs on another XCD and in another dispatch position; the answer must not
+    change."""
     plan = _hip.decode_plan(w.lengths, w.tables)
-    order = np.random.default_rng(seed).permutation(plan.shape[0])
-    return np.ascontiguousarray(plan[order])
+    return regrouped_plan(plan, np.random.default_rng(seed).permutation(8))
 
 
 @pytest.mark.parametrize("order", ["binned", "shuffled"])
 def test_batched_decode_b64_matches_oracle(device, order):
     """Batch 64, lengths U{1..2048}, fragmented tables over an 8192-block pool; every row
-    against the oracle restatement and FP64, with the plan as built and with its records
-    shuffled."""
+    against the oracle restatement and FP64, with the plan as built and with its groups of
+    bins moved to other XCDs."""
     _say("batched b64 plan", order)
     w = workloads.batched_decode(batch=64, num_blocks=8192)
     pool = _random_pool(device, w.num_blocks, 11)
@@ -310,14 +311,14 @@ def test_batched_decode_b64_matches_oracle(device, order):
     worst.report()
 
 
-def test_work_item_boundaries_match_oracle(device):
-    """Lengths on both sides of the 9-block (144-token) work-item boundaries -- one item
-    exactly filled, a one-token second item, 8, 9 and 15 items, a single token and a single
-    block -- in one ragged batch over a shuffled pool: every row against the oracle and
-    FP64."""
+def test_block_and_bin_boundaries_match_oracle(device):
+    """Lengths on both sides of 16-token block boundaries and of multiples of 9 blocks, a
+    single token and a single block, in one ragged batch over a shuffled pool: the plan cuts
+    the long rows across bins (parts merged in the kernel) and puts short rows several to a
+    bin; every row against the oracle and FP64."""
     lengths = np.array([143, 144, 145, 287, 288, 289, 1151, 1152, 1153, 1295, 1296, 1297, 2047, 2048, 1, 16],
                        dtype=np.int32)
-    _say("item boundaries", lengths.tolist())
+    _say("block and bin boundaries", lengths.tolist())
     need = (lengths + 15) // 16
     num_blocks = 1024
     perm = np.random.default_rng(77).permutation(num_blocks).astype(np.int32)
@@ -334,7 +335,10 @@ def test_work_item_boundaries_match_oracle(device):
     _hip.paged_decode_attention(out, queries, pool, layer, torch.from_numpy(tables).to(device),
                                 torch.from_numpy(lengths).to(device))
     torch.cuda.synchronize()
-    worst = Worst("work-item boundaries")
+    stats = check_decode_plan(_hip.decode_plan(lengths, tables), lengths, tables, num_blocks,
+                              _hip.workspace_bytes(len(lengths), tables.shape[1]))
+    assert stats["cut"] > 0
+    worst = Worst("block and bin boundaries")
     for b, (oracle, fp64) in _oracle_rows(pool, layer, w, queries, range(len(lengths))).items():
         worst.check(out[b : b + 1].reshape(1, 32, 1, 64), oracle, fp64, f"row {b} len {lengths[b]}")
     worst.report()
@@ -399,10 +403,10 @@ def _fp64_all_rows(pool, layer, tables, lengths, queries, chunk=32):
 def test_long_context_b256_full_length(device):
     """The long-context workload as one step of one layer: batch 256, each sequence 2047
     cached tokens on 128 blocks of a fully shuffled 40000-block pool; pc_kv_append writes
-    every sequence's new token (slot 2047), then attention runs over 2048 tokens (15 work
-    items each, several rounds of workgroups). The appended rows are bit-exact, every row
-    is within 2e-3 of FP64, sampled rows within 2e-3 of the op-for-op oracle, and a
-    shuffled plan gives the same bits."""
+    every sequence's new token (slot 2047), then attention runs over 2048 tokens (one bin
+    of 128 blocks per sequence). The appended rows are bit-exact, every row is within 2e-3
+    of FP64, sampled rows within 2e-3 of the op-for-op oracle, and regrouped bins give the
+    same bits."""
     _say("b256 long context: append + attention")
     w = workloads.batched_decode(batch=256, num_blocks=40000, fixed_length=2048, seed=44)
     pool = _random_pool(device, w.num_blocks, 12)
@@ -443,8 +447,9 @@ def test_long_context_b256_full_length(device):
 
 def test_plan_order_and_graph_replays_are_invisible(device):
     """Ragged lengths with empty, one-token, block-boundary and full rows: the output is the
-    same bits for the plan as built, for its records reversed, and for every replay of a
-    captured HIP graph (with eager calls in between), and matches the oracle."""
+    same bits for the plan as built, for its groups of bins in reverse XCD order, and for
+    every replay of a captured HIP graph (with eager calls in between), and matches the
+    oracle."""
     _say("plan order and graph replays")
     w = workloads.batched_decode(batch=64, num_blocks=8192, seed=49)
     lengths = w.lengths.copy()
@@ -459,7 +464,7 @@ def test_plan_order_and_graph_replays_are_invisible(device):
     _hip.paged_decode_attention(first, queries, pool, 9, tables, lens, plan=torch.from_numpy(plan).to(device))
     reversed_out = torch.full_like(queries, 7.0)
     _hip.paged_decode_attention(
-        reversed_out, queries, pool, 9, tables, lens, plan=torch.from_numpy(np.ascontiguousarray(plan[::-1])).to(device)
+        reversed_out, queries, pool, 9, tables, lens, plan=torch.from_numpy(regrouped_plan(plan, list(range(7, -1, -1)))).to(device)
     )
     torch.cuda.synchronize()
     assert torch.equal(first, reversed_out)
@@ -578,3 +583,126 @@ def test_batched_api_matches_single_request_api(device):
     for row, request in enumerate(requests):
         single = paged_attention(query[row : row + 1], allocator, request, layer_index=4)
         assert torch.equal(single, batched[row : row + 1])
+
+
+def _flags_clear(workspace) -> bool:
+    """Every partial slot's ready flag (4 bytes at offset 2112 of each 2176-byte slot) is
+    zero: the state each call must leave for the next."""
+    slots = workspace.numel() // 2176
+    return not workspace[: slots * 2176].view(slots, 2176)[:, 2112:2116].any().item()
+
+
+def _permuted_tables(lengths, num_blocks, seed):
+    need = [(int(x) + 15) // 16 for x in lengths]
+    perm = np.random.default_rng(seed).permutation(num_blocks).astype(np.int32)
+    tables = np.zeros((len(lengths), max(max(need), 1)), dtype=np.int32)
+    offset = 0
+    for b, n in enumerate(need):
+        tables[b, :n] = perm[offset : offset + n]
+        offset += n
+    return tables
+
+
+@pytest.mark.parametrize(
+    "lengths,num_blocks",
+    [
+        ([32768 - 5], 2100),  # one sequence: 256 bins of one group, merged from 256 parts
+        ([20000, 1, 5000, 16, 17, 8191], 2400),
+    ],
+    ids=["one-sequence", "mixed"],
+)
+def test_long_sequences_cut_over_many_bins(device, lengths, num_blocks):
+    """Sequences far longer than a bin: every part but the last goes through the workspace
+    and the last bin folds up to 255 of them. Every row within 2e-3 of FP64, two calls on
+    the same workspace give the same bits, and both leave the part flags at zero."""
+    lengths = np.asarray(lengths, dtype=np.int32)
+    _say("long sequences", lengths.tolist())
+    tables = _permuted_tables(lengths, num_blocks, 81)
+    stats = check_decode_plan(_hip.decode_plan(lengths, tables), lengths, tables, num_blocks,
+                              _hip.workspace_bytes(len(lengths), tables.shape[1]))
+    assert stats["cut"] >= 1
+    pool = _random_pool(device, num_blocks, 19)
+    layer = 13
+    gen = torch.Generator(device=device).manual_seed(7)
+    queries = torch.randn((len(lengths), 32, 64), dtype=torch.float16, device=device, generator=gen)
+    workspace = torch.zeros(_hip.workspace_bytes(len(lengths), tables.shape[1]), dtype=torch.uint8, device=device)
+    outs = []
+    for _ in range(2):
+        out = torch.full_like(queries, float("nan"))
+        _hip.paged_decode_attention(out, queries, pool, layer, torch.from_numpy(tables).to(device),
+                                    torch.from_numpy(lengths).to(device), workspace=workspace)
+        torch.cuda.synchronize()
+        assert _flags_clear(workspace)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+    worst = Worst(f"long sequences {lengths.tolist()}")
+    fp64 = _fp64_all_rows(pool, layer, tables, lengths, queries, chunk=1)
+    for b in range(len(lengths)):
+        worst.check(outs[0][b], None, fp64[b], f"row {b} len {lengths[b]}")
+    worst.report()
+
+
+def test_many_short_sequences_close_bins_early(device):
+    """1000 sequences of 1..48 tokens: a bin closes at 4 sequences before its nominal end,
+    so the plan has more bins than CUs. Every row within 2e-3 of FP64, sampled rows of the
+    oracle."""
+    rng = np.random.default_rng(82)
+    lengths = rng.integers(1, 49, size=1000).astype(np.int32)
+    lengths[:4] = [1, 16, 17, 48]
+    num_blocks = 3000
+    tables = _permuted_tables(lengths, num_blocks, 83)
+    plan = _hip.decode_plan(lengths, tables)
+    stats = check_decode_plan(plan, lengths, tables, num_blocks, _hip.workspace_bytes(len(lengths), tables.shape[1]))
+    assert stats["rows"] > 256 and (plan[:, 0] == 4).sum() > 0
+    _say("many short sequences", stats)
+    pool = _random_pool(device, num_blocks, 20)
+    w = workloads.BatchedDecode(lengths, tables, num_blocks, 84)
+    queries = torch.from_numpy(w.queries(2)).to(device)
+    out = torch.full_like(queries, float("nan"))
+    _hip.paged_decode_attention(out, queries, pool, 2, torch.from_numpy(tables).to(device),
+                                torch.from_numpy(lengths).to(device), plan=torch.from_numpy(plan).to(device))
+    torch.cuda.synchronize()
+    worst = Worst("1000 short sequences")
+    fp64 = _fp64_all_rows(pool, 2, tables, lengths, queries)
+    for b in range(len(lengths)):
+        worst.check(out[b], None, fp64[b], f"row {b} len {lengths[b]}")
+    for b, (oracle, _) in _oracle_rows(pool, 2, w, queries, [0, 1, 2, 3, 500, 999]).items():
+        worst.oracle = max(worst.oracle, assert_max_abs(out[b : b + 1].reshape(1, 32, 1, 64), oracle, f"row {b} vs oracle"))
+    worst.report()
+
+
+@pytest.mark.parametrize("where", ["first part", "middle part", "last part"])
+def test_bad_block_in_a_cut_sequence_poisons_only_its_row(device, where):
+    """An out-of-pool id in one part of a sequence cut over three or more bins: the merged
+    row is NaN, every other row (including those sharing its bins) keeps its bits, and the
+    part flags end at zero."""
+    w = workloads.batched_decode(batch=64, num_blocks=8192, seed=85)
+    plan = _hip.decode_plan(w.lengths, w.tables)
+    spans = {}
+    for r in range(plan.shape[0]):
+        for s in range(int(plan[r, 0])):
+            b, _, j0, n, _, kidx, nspan, _ = (int(v) for v in plan[r, 8 + 8 * s : 16 + 8 * s])
+            if nspan >= 3:
+                spans.setdefault(b, {})[kidx] = (j0, n, nspan)
+    assert spans, "the workload cuts no sequence over three bins"
+    b = min(spans)
+    nspan = spans[b][0][2]
+    kidx = {"first part": 0, "middle part": 1, "last part": nspan - 1}[where]
+    j0, n, _ = spans[b][kidx]
+    _say("bad block in", where, "of row", b, "parts", nspan, "block", j0 + n // 2)
+    pool = _random_pool(device, w.num_blocks, 21)
+    queries = torch.from_numpy(w.queries(6)).to(device)
+    lens = torch.from_numpy(w.lengths).to(device)
+    workspace = torch.zeros(_hip.workspace_bytes(w.batch, w.tables.shape[1]), dtype=torch.uint8, device=device)
+    good = torch.empty_like(queries)
+    _hip.paged_decode_attention(good, queries, pool, 6, torch.from_numpy(w.tables).to(device), lens, workspace=workspace)
+    broken = w.tables.copy()
+    broken[b, j0 + n // 2] = w.num_blocks + 3
+    bad = torch.empty_like(queries)
+    _hip.paged_decode_attention(bad, queries, pool, 6, torch.from_numpy(broken).to(device), lens, workspace=workspace)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad[b]).all()
+    others = [x for x in range(w.batch) if x != b]
+    assert torch.equal(bad[others], good[others])
+    assert not torch.isnan(good).any()
+    assert _flags_clear(workspace)

@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 
 from pagedcore_amd import _hip
+from tests.bin_plan import ROW, check_decode_plan
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -31,17 +32,28 @@ def test_library_exports_every_declared_symbol():
     assert lib.pc_abi_version() == _hip.ABI_VERSION
 
 
-def test_workspace_size_formula():
+def _slots_bound(batch, max_blocks):
+    """Partial slots a plan of the shape can need: at most one per bin (only a bin's last
+    segment can be a part that is not its sequence's last), and the bins number at most 256
+    plus one per 256 blocks, 2 per group for rounding, and one early close per 3 sequences."""
+    total = batch * max_blocks
+    return 256 + -(-total // 256) + 16 + (batch + 2) // 3
+
+
+def test_workspace_and_capacity_formulas():
     lib = _hip.load()
-    # one fp32 partial per (sequence, kv head, 9-block work item): O [8 q heads][64] then
-    # (max, sum) of the 8 q heads
-    part = (8 * 64 + 16) * 4
-    assert lib.pc_attn_workspace_bytes(64, 128) == 64 * 4 * 15 * part
-    assert lib.pc_attn_workspace_bytes(1, 9) == 4 * part
-    assert lib.pc_attn_workspace_bytes(1, 10) == 4 * 2 * part
-    assert lib.pc_attn_workspace_bytes(0, 128) == 0
+    # one partial slot per (cut part, kv head): fp32 O of 8 q heads x 64 dims (2 KiB), then
+    # (max, sum) of the 8 q heads, then the part's ready flag, padded to 17 128-byte lines
+    slot = 2048 + 64 + 64
+    assert slot == 2176
+    for batch, blocks in ((64, 128), (1, 9), (1, 10), (256, 128), (97, 128), (0, 128)):
+        assert lib.pc_attn_workspace_bytes(batch, blocks) == _slots_bound(batch, blocks) * 4 * slot
+        group = max(256, -(-batch * blocks // 256)) + 1 + (batch + 2) // 3 + 1
+        assert lib.pc_attn_plan_capacity(batch, blocks) == 8 * group
+    assert lib.pc_attn_workspace_bytes(64, 128) < 3 << 20  # a few MiB, independent of context length
     for batch, blocks in ((-1, 8), (1, 0), (1, 65537)):
         assert lib.pc_attn_workspace_bytes(batch, blocks) == 0
+        assert lib.pc_attn_plan_capacity(batch, blocks) == -1
 
 
 @pytest.mark.parametrize(
@@ -75,7 +87,7 @@ def test_append_rejects_invalid_arguments_without_a_gpu(args, needle):
         ({"plan": 260}, b"aligned"),
         ({"blocks": 2**31}, b"num_blocks"),
         ({"nrec": -1}, b"num_records"),
-        ({"nrec": (1 + 8) * 15 + 1}, b"num_records"),  # batch 1, 128 blocks: 15 items per sequence
+        ({"nrec": 8 * (256 + 1 + 1 + 1) + 1}, b"num_records"),  # batch 1, 128 blocks: capacity + 1
     ],
 )
 def test_attention_rejects_invalid_arguments_without_a_gpu(overrides, needle):
@@ -91,73 +103,78 @@ def test_attention_rejects_invalid_arguments_without_a_gpu(overrides, needle):
     assert needle in lib.pc_last_error()
 
 
-def _items_by_enumeration(lengths, tables):
-    """Every (sequence, item) record written out directly: {row, item, length, items of the
-    row, the item's 9 block ids (past the row's last block: its last id), 0, 0, 0}."""
-    records = {}
-    for b, length in enumerate(lengths):
-        if length <= 0:
-            continue
-        blocks = min(-(-int(length) // 16), tables.shape[1])
-        items = -(-blocks // 9)
-        for item in range(items):
-            ids = [int(tables[b, min(item * 9 + i, blocks - 1)]) for i in range(9)]
-            records[(b, item)] = tuple([b, item, int(length), items] + ids + [0, 0, 0])
-    return records
+def _plan_and_check(lengths, tables, num_blocks):
+    lib = _hip.load()
+    plan = _hip.decode_plan(lengths, tables)
+    assert plan.dtype == np.int32 and plan.shape[1] == lib.pc_attn_plan_record_ints() == ROW
+    assert plan.shape[0] <= lib.pc_attn_plan_capacity(len(lengths), tables.shape[1])
+    workspace = lib.pc_attn_workspace_bytes(len(lengths), tables.shape[1])
+    return plan, check_decode_plan(plan, lengths, tables, num_blocks, workspace)
 
 
-def test_decode_plan_lists_every_item_once_on_one_bin_per_sequence():
-    """pc_attn_plan (host code) against a direct enumeration, on ragged lengths including
-    zero-length rows, exact block multiples and the full 128-block table width: every
-    item appears once, the items of a sequence share record index modulo 8 (one XCD), the
-    8 bins' item counts differ by at most one sequence's items, padding records are empty,
-    and longer sequences are dealt first."""
+def test_decode_plan_covers_every_block_once_in_balanced_bins():
+    """pc_attn_plan (host code) on ragged lengths including zero-length rows, exact block
+    multiples and the full 128-block table width: every block of every sequence appears
+    once, in order, with its table id; a cut sequence's parts sit in one group (one XCD) at
+    rows first bin + 8 k; only a bin's first and last segments are cut parts; partial slots
+    lie inside the workspace and do not overlap; the bins' block counts are balanced."""
     rng = np.random.default_rng(5)
     lengths = rng.integers(0, 2049, size=97).astype(np.int32)
     lengths[:6] = [0, 1, 16, 17, 2048, 2047]
     tables = rng.integers(0, 50000, size=(97, 128)).astype(np.int32)
-    plan = _hip.decode_plan(lengths, tables)
-    lib = _hip.load()
-    assert plan.dtype == np.int32 and plan.shape[1] == lib.pc_attn_plan_record_ints() == 16
-    assert plan.shape[0] % 8 == 0 and plan.shape[0] <= lib.pc_attn_plan_capacity(97, 128)
-    expected = _items_by_enumeration(lengths, tables)
-    live = [tuple(r) for r in plan.tolist() if r[0] >= 0]
-    assert sorted(live) == sorted(expected.values())
-    for r in plan.tolist():
-        if r[0] < 0:
-            assert r == [-1] + [0] * 15
-    bin_of = {}
-    for index, r in enumerate(plan.tolist()):
-        if r[0] >= 0:
-            assert bin_of.setdefault(r[0], index % 8) == index % 8, "items of a sequence on two bins"
-    per_bin = [sum(1 for index, r in enumerate(plan.tolist()) if r[0] >= 0 and index % 8 == x) for x in range(8)]
-    assert max(per_bin) - min(per_bin) <= 15
-    first_seen = {}
-    for index, r in enumerate(plan.tolist()):
-        if r[0] >= 0:
-            first_seen.setdefault(r[0], index // 8)
-    # within a bin, rows appear in order of decreasing length
-    for x in range(8):
-        rows = sorted((first_seen[b], b) for b in bin_of if bin_of[b] == x)
-        lens = [lengths[b] for _, b in rows]
-        assert lens == sorted(lens, reverse=True)
+    plan, stats = _plan_and_check(lengths, tables, 50000)
+    # 256 bins of about 24 blocks (one per CU), and an early close or two where a bin
+    # would hold more than 4 sequences
+    assert 256 <= stats["rows"] <= 8 * 34 and stats["cut"] > 0
+    blocks = plan[:, 1][plan[:, 0] > 0]
+    nominal = -(-int(plan[:, 1].sum()) // 256)
+    assert blocks.max() <= nominal + 1
+
+
+@pytest.mark.parametrize(
+    "name,lengths,max_blocks",
+    [
+        ("one token", [1], 8),
+        ("one long sequence", [2048 * 16], 2048),
+        ("many short sequences", [16] * 1000 + [1] * 24, 4),
+        ("short and long", [17] * 300 + [2048] * 8, 128),
+        ("long-context batch", [2048] * 256, 128),
+        ("all empty", [0] * 7, 16),
+        ("maximum table", [65536 * 16, 3, 0], 65536),
+    ],
+)
+def test_decode_plan_edge_shapes(name, lengths, max_blocks):
+    """Shapes that stress the planner's bounds: a single block, one sequence cut over many
+    bins, more sequences than 4 per bin allows (early closes), a mix, a batch of whole
+    sequences, an empty batch and the maximum table width; every plan passes the full check
+    and fits the advertised capacity and workspace."""
+    lengths = np.asarray(lengths, dtype=np.int32)
+    rng = np.random.default_rng(len(lengths))
+    tables = rng.integers(0, 1 << 20, size=(len(lengths), max_blocks)).astype(np.int32)
+    plan, stats = _plan_and_check(lengths, tables, 1 << 20)
+    if lengths.max() == 0:
+        assert plan.shape[0] == 0
+    else:
+        assert plan.shape[0] % 8 == 0 and stats["rows"] == plan.shape[0]
 
 
 def test_decode_plan_rejects_bad_arguments():
     lib = _hip.load()
     lens = np.array([100, 200], dtype=np.int32)
     tables = np.zeros((2, 16), dtype=np.int32)
-    records = np.zeros((64, 16), dtype=np.int32)
+    records = np.zeros((64, ROW), dtype=np.int32)
     plan = lib.pc_attn_plan
-    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, records.ctypes.data, 8) == -1  # needs 16 records
+    # 7 + 13 blocks: 2 bins (8 blocks or more each, one whole sequence in each), in two
+    # groups; one row per group, so 8 rows
+    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, records.ctypes.data, 7) == -1
     assert b"capacity" in lib.pc_last_error()
-    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, records.ctypes.data, 16) == 16
+    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, records.ctypes.data, 8) == 8
     assert plan(lens.ctypes.data, tables.ctypes.data, 2, 0, records.ctypes.data, 64) == -1
     assert b"max_blocks" in lib.pc_last_error()
     assert plan(None, tables.ctypes.data, 2, 16, records.ctypes.data, 64) == -1
     assert plan(lens.ctypes.data, None, 2, 16, records.ctypes.data, 64) == -1
     assert b"null" in lib.pc_last_error()
-    assert lib.pc_attn_plan_capacity(2, 16) == (2 + 8) * 2
+    assert lib.pc_attn_plan_capacity(2, 16) == 8 * (256 + 1 + 1 + 1)
     assert lib.pc_attn_plan_capacity(2, 0) == -1
     assert plan(None, None, 0, 16, None, 0) == 0  # empty batch: nothing to plan
     # a context longer than its table (16 tokens per entry) is refused, not clamped, and the
@@ -167,7 +184,7 @@ def test_decode_plan_rejects_bad_arguments():
         assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, records.ctypes.data, 64) == -1
         assert b"exceeds its 16-block table" in lib.pc_last_error()
     lens[1] = 16 * 16
-    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, records.ctypes.data, 64) == 16
+    assert plan(lens.ctypes.data, tables.ctypes.data, 2, 16, records.ctypes.data, 64) == 8
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
@@ -202,8 +219,9 @@ def test_noalloc_attention_refuses_oversize_shapes_before_any_hip_call():
     """The allocation-free entry point checks the shape against its 32 MiB device array
     first, so the refusal needs no GPU (nothing else is touched)."""
     lib = _hip.load()
-    assert lib.pc_attn_workspace_bytes(512, 128) > 32 << 20
-    status = lib.pc_paged_decode_attn_noalloc(None, None, None, 8, 0, None, 512, 128, None, 1, None)
+    assert lib.pc_attn_workspace_bytes(8192, 128) > 32 << 20
+    assert lib.pc_attn_workspace_bytes(4096, 128) <= 32 << 20
+    status = lib.pc_paged_decode_attn_noalloc(None, None, None, 8, 0, None, 8192, 128, None, 1, None)
     assert status == 1 and b"allocation-free entry point holds" in lib.pc_last_error()
     assert lib.pc_paged_decode_attn_noalloc(None, None, None, 8, 0, None, 1, 0, None, 1, None) == 1
     assert b"max_blocks" in lib.pc_last_error()

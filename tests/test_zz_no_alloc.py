@@ -20,6 +20,7 @@ from tests import workloads
 pytestmark = pytest.mark.gpu
 
 SCRATCH_BYTES = 32 << 20  # PC_ATTN_NOALLOC_SCRATCH_BYTES
+SLOT_BYTES, FLAG_OFFSET = 2176, 2112  # a partial slot and its ready flag's offset in it
 
 
 def _say(*parts) -> None:
@@ -48,15 +49,16 @@ def _call(lib, name, out, queries, pool, layer, lens, w, plan, *workspace):
 
 def test_noalloc_entry_point_matches_the_workspace_entry_point(device):
     lib = _hip.load()
-    # First call: batch 64 over the full 2048-token range (15-item sequences); second call:
-    # a smaller batch with shorter tables, so the array still holds the first call's
-    # partials in places the second call does not write.
+    # First call: batch 64 over the full 2048-token range (long rows cut over several bins,
+    # their parts merged through the array); second call: a smaller batch with shorter
+    # tables, so the array still holds the first call's partials in places the second call
+    # does not write.
     for batch, hi, num_blocks, seed, layer in ((64, 2048, 8192, 61, 4), (9, 500, 1024, 62, 17)):
         _say("no-alloc call", batch, hi)
         w, pool, queries, plan, lens = _inputs(device, batch, hi, num_blocks, seed, layer)
         nbytes = int(lib.pc_attn_workspace_bytes(w.batch, int(w.tables.shape[1])))
         assert 0 < nbytes <= SCRATCH_BYTES
-        workspace = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=device)
+        workspace = torch.zeros((nbytes,), dtype=torch.uint8, device=device)
         expected = torch.full_like(queries, float("nan"))
         _call(lib, "pc_paged_decode_attn", expected, queries, pool, layer, lens, w, plan, workspace.data_ptr())
         got = torch.full_like(queries, float("nan"))
@@ -66,6 +68,9 @@ def test_noalloc_entry_point_matches_the_workspace_entry_point(device):
         torch.cuda.synchronize(device)
         assert torch.cuda.memory_allocated(device) == allocated
         assert torch.equal(got.view(torch.int16), expected.view(torch.int16))
+        # the workspace call left every part flag at zero again (the next call relies on it)
+        flags = workspace.view(-1, SLOT_BYTES)[:, FLAG_OFFSET : FLAG_OFFSET + 4]
+        assert not flags.any().item()
         # and both within 2e-3 of FP64 on a few rows (the kernels' own parity bar)
         for b in (0, w.batch // 2, w.batch - 1):
             length = int(w.lengths[b])
@@ -81,11 +86,11 @@ def test_noalloc_entry_point_matches_the_workspace_entry_point(device):
 
 def test_noalloc_entry_point_refuses_shapes_beyond_its_array(device):
     lib = _hip.load()
-    # batch 512 with 128-block tables needs 64.9 MB of partials: refused before any launch
-    assert lib.pc_attn_workspace_bytes(512, 128) > SCRATCH_BYTES
+    # batch 8192 with 128-block tables needs 61.8 MB of partial slots: refused before any launch
+    assert lib.pc_attn_workspace_bytes(8192, 128) > SCRATCH_BYTES
     out = torch.empty(16, dtype=torch.float16, device=device)
     status = lib.pc_paged_decode_attn_noalloc(
-        out.data_ptr(), out.data_ptr(), out.data_ptr(), 8, 0, out.data_ptr(), 512, 128, out.data_ptr(), 1,
+        out.data_ptr(), out.data_ptr(), out.data_ptr(), 8, 0, out.data_ptr(), 8192, 128, out.data_ptr(), 1,
         torch.cuda.current_stream(device).cuda_stream,
     )
     assert status == 1
