@@ -71,21 +71,27 @@ int pc_kv_append(void* pool, int64_t num_blocks, int32_t layer_begin, int32_t nu
  *   query        [batch][32][64] fp16, contiguous; q head h reads kv head h / 8
  *   out          [batch][32][64] fp16, contiguous (query, out, pool and plan 16-byte aligned)
  *   context_lens [batch] int32 device copy of the lengths the plan was built from
- *                (0 or less: the row is not written)
- *   plan         num_records records of pc_attn_plan_record_ints() int32 from pc_attn_plan()
- *                for the same lengths and block tables (device copy); one plan serves every
- *                layer of a decode step
+ *                (0 or less: the row is not written); the kernel takes the lengths from
+ *                the plan, which carries them
+ *   plan         num_records rows of pc_attn_plan_record_ints() int32 from pc_attn_plan()
+ *                for the same lengths and block tables (device copy), optionally followed
+ *                by all-zero padding rows; one plan serves every layer of a decode step
  *   out[b][h] = softmax(q[b][h] . K[b][:len]^T / 8) . V[b][:len], computed in fp32 and
  *   rounded once to fp16. Slots past len are never multiplied, so poisoned (NaN) tail
  *   slots do not reach the output. A block id outside [0, num_blocks) is never
  *   dereferenced; its sequence's output rows become NaN. A plan that does not match
  *   context_lens gives wrong rows, never an access outside the buffers.
  *
- * Split-K: a sequence is cut into work items of 9 blocks, one workgroup each. A sequence
- * of one item is written directly; longer ones leave one fp32 partial per item and kv head
- * in `workspace` (pc_attn_workspace_bytes() bytes, 256-byte aligned, scratch whose contents
- * do not matter between calls; may be null when max_blocks <= 9), merged by a second kernel
- * launched on the same stream. Calls that share a workspace must not overlap.
+ * One kernel launch, one workgroup per plan row (a bin of up to 256 blocks and 4
+ * sequences). A sequence cut over several bins of one group leaves one fp32 partial per
+ * part (all but its last) and kv head in `workspace`, with a ready flag; the bin holding
+ * its last part waits for the flags (a bounded wait), folds the parts in order and writes
+ * the row, then sets the flags back to zero. `workspace`: pc_attn_workspace_bytes() bytes,
+ * 256-byte aligned, required (never null), ALL ZERO before its first use (hipMemset, or a
+ * fill kernel under graph capture); every call leaves its flags at zero again, so it is
+ * reused as is. Calls that share a workspace must not overlap in time. A part found
+ * flagged by another XCD, or not flagged within the bounded wait, turns its sequence's rows
+ * into NaN instead of reading a partial that may not be visible.
  */
 int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t num_blocks, int32_t layer,
                          const int32_t* context_lens, int32_t batch, int32_t max_blocks, const int32_t* plan,
@@ -104,8 +110,10 @@ int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks);
  * PC_ATTN_NOALLOC_SCRATCH_BYTES bytes, held until the process ends; its address is looked
  * up once per device (hipGetSymbolAddress) on the first call there. The call allocates and
  * frees nothing. Shapes whose workspace (pc_attn_workspace_bytes) exceeds the array are
- * refused with PC_ERR_ARGUMENT before any HIP call (32 MiB covers, e.g., batch 256 with
- * 128-block tables). `stream` must belong to the current device. Every call on one GPU
+ * refused with PC_ERR_ARGUMENT before any HIP call (32 MiB covers, e.g., batch 4096 with
+ * 128-block tables, but not batch 8192). The array starts at zero when the library loads
+ * and every call leaves its flags at zero. `stream` must belong to the current device.
+ * Every call on one GPU
  * shares that GPU's array: calls that overlap in time on one GPU (concurrent streams,
  * threads) race and give wrong rows; calls ordered on one stream are safe. Arguments and
  * results are otherwise those of pc_paged_decode_attn.
@@ -118,20 +126,24 @@ int pc_paged_decode_attn_noalloc(void* out, const void* query, const void* pool,
 /*
  * Host-side decode plan (no device access). context_lens [batch] and block_tables
  * [batch][max_blocks] are HOST arrays (row b: sequence b's physical blocks in logical order,
- * only the first ceil(len / 16) read); plan is HOST memory of `capacity` records. Writes one
- * record of pc_attn_plan_record_ints() int32 per work item,
- *   {sequence, item, context length, items of the sequence, 9 block ids (past the
- *    sequence's last block: its last id), 0, 0, 0},
- * dealing sequences (longest first) to 8 bins of balanced item counts so that all items of
- * a sequence run on one XCD; bins are interleaved record by record and padded with records
- * whose sequence is -1. Returns the record count, or -pc_status on invalid arguments
- * (including a context length above 16 * max_blocks: its table cannot hold it) or if
- * `capacity` is too small; pc_attn_plan_capacity() always suffices (-1 on invalid
- * arguments).
+ * only the first ceil(len / 16) read); plan is HOST memory of `capacity` rows of
+ * pc_attn_plan_record_ints() (296) int32. Sequences are dealt, longest first, to the least
+ * loaded of 8 groups (one per XCD); each group's blocks, taken sequence after sequence, are
+ * cut into bins of equal block counts (about total / 256 blocks each, at least 8, at most
+ * 256, and a bin also closes at 4 sequences). Row r holds bin r / 8 of group r % 8:
+ *   {segments, blocks, 0 x 6},
+ *   4 segments {sequence, context length, first block, blocks, row of the sequence's first
+ *               bin, part index, parts, first partial slot (cut sequences) or 0},
+ *   the bin's block ids in order (up to 256; 0 past them).
+ * A cut sequence's part k is in row first + 8 k; only a bin's first and last segments can
+ * be cut parts. Groups with fewer bins are padded with all-zero rows. Returns the row
+ * count (a multiple of 8), or -pc_status on invalid arguments (including a context length
+ * above 16 * max_blocks: its table cannot hold it) or if `capacity` is too small;
+ * pc_attn_plan_capacity() always suffices (-1 on invalid arguments).
  *
  * Replaces nothing in the reference: PagedCore walks each sequence's pages in Python
  * (reference src/pagedcore/attention.py:31-53); the plan is what lets one launch cover a
- * ragged batch with every block load issued at once.
+ * ragged batch with every CU streaming the same number of blocks.
  */
 int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, int32_t batch, int32_t max_blocks,
                      int32_t* plan, int64_t capacity);
