@@ -240,12 +240,6 @@ __device__ __host__ __forceinline__ int blocks_of(int len) { return len / kSlots
 
 // One uniform int32 by a scalar load that bypasses the scalar cache (sees L2; waits on
 // lgkmcnt only, so the ring's loads stay counted).
-__device__ __forceinline__ int sload_glc(const int32_t* p) {
-  int v;
-  asm volatile("s_load_dword %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
-  return v;
-}
-
 __device__ __forceinline__ int xcc_id() {
   int v;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
@@ -337,12 +331,24 @@ __device__ __forceinline__ void store_part(char* slot, int lane, const Part& p) 
   }
 }
 
-__device__ __forceinline__ void load_part(const char* slot, int lane, Part& p) {
+// A partial staged in LDS by stage_part: lane L's O at 16 L and 1024 + 16 L, lane L's
+// copy of (m, l) word L % 16 at 2048 + 4 L (words 0-3 m of q heads 0-3, 4-7 their l, 8-11 m
+// of q heads 4-7, 12-15 their l).
+constexpr int kStageBytes = 2048 + 256;
+constexpr int kStageParts = kWaveLds / kStageBytes;  // partials per round trip of a merge (7)
+
+__device__ __forceinline__ void stage_part(const char* slot, int lane, char* dst) {
+  __builtin_amdgcn_global_load_lds(static_cast<const void*>(slot + lane * 32), lds_ptr(dst), 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(static_cast<const void*>(slot + lane * 32 + 16), lds_ptr(dst + 1024), 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(static_cast<const void*>(slot + 2048 + 4 * (lane & 15)), lds_ptr(dst + 2048), 4, 0, 0);
+}
+
+__device__ __forceinline__ void read_staged_part(const char* src, int lane, Part& p) {
+  const float4_t a = *reinterpret_cast<const float4_t*>(src + lane * 16);
+  const float4_t b = *reinterpret_cast<const float4_t*>(src + 1024 + lane * 16);
   const int gh = (lane >> 4) & 1;
-  const float4_t a = *reinterpret_cast<const float4_t*>(slot + lane * 32);
-  const float4_t b = *reinterpret_cast<const float4_t*>(slot + lane * 32 + 16);
-  const float4_t m = *reinterpret_cast<const float4_t*>(slot + 2048 + gh * 32);
-  const float4_t l = *reinterpret_cast<const float4_t*>(slot + 2048 + gh * 32 + 16);
+  const float4_t m = *reinterpret_cast<const float4_t*>(src + 2048 + 32 * gh);
+  const float4_t l = *reinterpret_cast<const float4_t*>(src + 2048 + 32 * gh + 16);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     p.o[0][r] = a[r];
@@ -589,7 +595,8 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
                          __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  // Sequences complete within the bin: their fp16 rows from LDS.
+  // Sequences complete within the bin: their fp16 rows from LDS (before the merge, which
+  // stages partials over the whole wave area).
   wave_lds_fence();
 #pragma unroll
   for (int s = 0; s < kMaxSegs; ++s) {
@@ -604,27 +611,47 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
   if (complete && nspan0 > 1 && kidx0 == nspan0 - 1 && slots_ok(slot0, nspan0) &&
       k00 + static_cast<int64_t>(kGroups) * kidx0 == static_cast<int64_t>(blockIdx.x) && k00 >= 0) {
     const int want = 1 + ((xcc_id() + 1) << 8);
+    const int nparts = nspan0 - 1;  // parts 0 .. nspan0 - 2 are in the workspace
+    // The flags: lane k polls part base + k's (lanes past the span repeat the last part's),
+    // 64 per load, until all are raised.
     bool ok = true;
-    for (int k = 0; k < nspan0 - 1; ++k) {
-      const int32_t* flag = reinterpret_cast<const int32_t*>(part_slot(slots, slot0, k, h) + kFlagOffset);
+    for (int base = 0; base < nparts; base += 64) {
+      const int32_t* flag =
+          reinterpret_cast<const int32_t*>(part_slot(slots, slot0, min(base + lane, nparts - 1), h) + kFlagOffset);
       int f = 0;
+#pragma nounroll
       for (int spins = 0; spins < kMaxSpins; ++spins) {
-        f = sload_glc(flag);
-        if (f != 0) break;
+        f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_ballot_w64(f == 0) == 0) break;
         __builtin_amdgcn_s_sleep(2);
       }
-      if (f != want) ok = false;  // never raised, or raised on another XCD (its partial is not visible here)
+      // never raised, or raised on another XCD (its partial is not visible here)
+      if (__builtin_amdgcn_ballot_w64(f != want) != 0) ok = false;
     }
+    // The partials, kStageParts per round trip, staged in the wave's LDS (free after the
+    // stream) by DMA and folded in span order. The loops stay rolled: this code runs once
+    // per merge, cold in the instruction cache, where every 64-byte line fetched costs an
+    // L2 round trip.
     Part acc_p;
-    for (int k0s = 0; k0s < nspan0 - 1; k0s += 8) {
-      Part pp[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) load_part(part_slot(slots, slot0, min(k0s + i, nspan0 - 2), h), lane, pp[i]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (k0s + i >= nspan0 - 1) break;
-        if (k0s + i == 0) acc_p = pp[i]; else fold_part(acc_p, pp[i]);
+    for (int r = 0; r < 4; ++r) {
+      acc_p.m[r] = -INFINITY;
+      acc_p.l[r] = 0.f;
+      acc_p.o[0][r] = 0.f;
+      acc_p.o[1][r] = 0.f;
+    }
+    for (int c0 = 0; c0 < nparts; c0 += kStageParts) {
+      const int cn = min(kStageParts, nparts - c0);
+#pragma nounroll
+      for (int i = 0; i < cn; ++i) stage_part(part_slot(slots, slot0, c0 + i, h), lane, wl + i * kStageBytes);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma nounroll
+      for (int i = 0; i < cn; ++i) {
+        Part pp;
+        read_staged_part(wl + i * kStageBytes, lane, pp);
+        fold_part(acc_p, pp);
       }
+      wave_lds_fence();  // the chunk's LDS reads are done before the next chunk's DMA
     }
     fold_part(acc_p, first_part);
     if (!ok) {
