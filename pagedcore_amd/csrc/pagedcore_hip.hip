@@ -806,32 +806,37 @@ int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, i
     int64_t nb = (target * load[x] + total / 2) / total;
     nb = std::max<int64_t>(nb, (load[x] + kMaxUnits - 1) / kMaxUnits);
     nb = std::max<int64_t>(1, std::min<int64_t>(nb, load[x]));
-    // Bin i nominally ends at block floor((i + 1) load / nb) of the group; a bin also closes
-    // when it holds kMaxSegs segments and the next block starts another sequence.
-    auto boundary_after = [&](int64_t pos) {
-      const int64_t i = (pos * nb) / load[x];  // first i with (i + 1) load / nb > pos
-      for (int64_t j = std::max<int64_t>(0, i - 1);; ++j) {
-        const int64_t e = ((j + 1) * load[x]) / nb;
-        if (e > pos) return e;
-      }
-    };
+    // Each bin takes the group's remaining blocks over its remaining bins (at most
+    // kMaxUnits); a bin also closes when it holds kMaxSegs segments and the next block starts
+    // another sequence. A bin that starts with the last part of a cut sequence merges that
+    // sequence's earlier parts after its own stream (about a third of a block's stream time
+    // per part, measured), so it takes (parts + 3) / 4 blocks fewer and the other bins share
+    // them.
     std::vector<BinSegs>& out = bins[x];
+    auto bin_end = [&](int64_t pos, int32_t seq_blocks, int32_t done, int32_t parts) {
+      const int64_t left = std::max<int64_t>(1, nb - static_cast<int64_t>(out.size()));
+      int64_t cap = (load[x] - pos + left - 1) / left;
+      if (done > 0 && seq_blocks - done <= cap) cap = std::max<int64_t>(seq_blocks - done, cap - (parts + 3) / 4);
+      return pos + std::min<int64_t>(std::max<int64_t>(cap, 1), kMaxUnits);
+    };
     BinSegs cur;
-    int64_t pos = 0, end = boundary_after(0);
+    int64_t pos = 0, end = -1;
     for (int32_t b : members[x]) {
       const int32_t n = blocks_of(context_lens[b]);
-      int32_t j = 0;
+      int32_t j = 0, parts = 0;
+      if (end < 0) end = bin_end(0, n, 0, 0);
       while (j < n) {
         if (cur.blocks > 0 && (pos == end || cur.nseg == kMaxSegs)) {
           out.push_back(cur);
           cur = BinSegs();
-          end = boundary_after(pos);
+          end = bin_end(pos, n, j, parts);
         }
         const int32_t take = static_cast<int32_t>(std::min<int64_t>(n - j, end - pos));
         cur.seg[cur.nseg][0] = b;
         cur.seg[cur.nseg][1] = j;
         cur.seg[cur.nseg][2] = take;
         ++cur.nseg;
+        ++parts;
         cur.blocks += take;
         j += take;
         pos += take;
