@@ -343,19 +343,70 @@ __device__ __forceinline__ void stage_part(const char* slot, int lane, char* dst
   __builtin_amdgcn_global_load_lds(static_cast<const void*>(slot + 2048 + 4 * (lane & 15)), lds_ptr(dst + 2048), 4, 0, 0);
 }
 
-__device__ __forceinline__ void read_staged_part(const char* src, int lane, Part& p) {
-  const float4_t a = *reinterpret_cast<const float4_t*>(src + lane * 16);
-  const float4_t b = *reinterpret_cast<const float4_t*>(src + 1024 + lane * 16);
-  const int gh = (lane >> 4) & 1;
-  const float4_t m = *reinterpret_cast<const float4_t*>(src + 2048 + 32 * gh);
-  const float4_t l = *reinterpret_cast<const float4_t*>(src + 2048 + 32 * gh + 16);
+// The staged partials [0, n) of one chunk, and the merging bin's own part last when
+// `with_own`, combined into one: their max M first (all reads issued at once), then, in part
+// order, each part's sum and O weighted by
+// 2^(m log2(e) / 8 - M log2(e) / 8). One wave per SIMD issues a VALU instruction every 4
+// cycles and waits out every LDS latency it does not overlap: this form costs about a third
+// of a pairwise online fold.
+__device__ __forceinline__ Part combine_staged(const char* stage, int n, int lane, const Part& own, bool with_own) {
+  const int ml = 2048 + 32 * ((lane >> 4) & 1);
+  float4_t mk[kStageParts];
+#pragma unroll
+  for (int i = 0; i < kStageParts; ++i) mk[i] = *reinterpret_cast<const float4_t*>(stage + min(i, n - 1) * kStageBytes + ml);
+  float4_t mx = mk[0];
+#pragma unroll
+  for (int i = 1; i < kStageParts; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx[r] = fmaxf(mx[r], mk[i][r]);
+  if (with_own) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx[r] = fmaxf(mx[r], own.m[r]);
+  }
+  Part c;
+  float neg[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    p.o[0][r] = a[r];
-    p.o[1][r] = b[r];
-    p.m[r] = m[r];
-    p.l[r] = l[r];
+    c.m[r] = mx[r];
+    c.l[r] = 0.f;
+    c.o[0][r] = 0.f;
+    c.o[1][r] = 0.f;
+    neg[r] = -mx[r] * kScoreToLog2;
   }
+  // Two parts per iteration (the second one's weight is 0 past the chunk): their eight LDS
+  // reads share one latency.
+#pragma nounroll
+  for (int i = 0; i < n; i += 2) {
+    const char* p0 = stage + i * kStageBytes;
+    const char* p1 = stage + min(i + 1, n - 1) * kStageBytes;
+    const float4_t a0 = *reinterpret_cast<const float4_t*>(p0 + lane * 16);
+    const float4_t b0 = *reinterpret_cast<const float4_t*>(p0 + 1024 + lane * 16);
+    const float4_t m0 = *reinterpret_cast<const float4_t*>(p0 + ml);
+    const float4_t l0 = *reinterpret_cast<const float4_t*>(p0 + ml + 16);
+    const float4_t a1 = *reinterpret_cast<const float4_t*>(p1 + lane * 16);
+    const float4_t b1 = *reinterpret_cast<const float4_t*>(p1 + 1024 + lane * 16);
+    const float4_t m1 = *reinterpret_cast<const float4_t*>(p1 + ml);
+    const float4_t l1 = *reinterpret_cast<const float4_t*>(p1 + ml + 16);
+    const bool second = i + 1 < n;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float s0 = exp2_fast(fmaf(m0[r], kScoreToLog2, neg[r]));
+      const float s1 = second ? exp2_fast(fmaf(m1[r], kScoreToLog2, neg[r])) : 0.f;
+      c.l[r] = fmaf(l1[r], s1, fmaf(l0[r], s0, c.l[r]));
+      c.o[0][r] = fmaf(a1[r], s1, fmaf(a0[r], s0, c.o[0][r]));
+      c.o[1][r] = fmaf(b1[r], s1, fmaf(b0[r], s0, c.o[1][r]));
+    }
+  }
+  if (with_own) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float s = exp2_fast(fmaf(own.m[r], kScoreToLog2, neg[r]));
+      c.l[r] = fmaf(own.l[r], s, c.l[r]);
+      c.o[0][r] = fmaf(own.o[0][r], s, c.o[0][r]);
+      c.o[1][r] = fmaf(own.o[1][r], s, c.o[1][r]);
+    }
+  }
+  return c;
 }
 
 // Workspace slot of part k of a cut sequence whose parts start at slot `first` (the plan
@@ -645,15 +696,18 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
 #pragma nounroll
       for (int i = 0; i < cn; ++i) stage_part(part_slot(slots, slot0, c0 + i, h), lane, wl + i * kStageBytes);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma nounroll
-      for (int i = 0; i < cn; ++i) {
-        Part pp;
-        read_staged_part(wl + i * kStageBytes, lane, pp);
-        fold_part(acc_p, pp);
+      // A span of at most kStageParts earlier parts is one chunk, combined with this bin's
+      // own part; longer spans fold their chunks' results in order, then the own part.
+      const bool single = nparts <= kStageParts;
+      const Part cp = combine_staged(wl, cn, lane, first_part, single);
+      if (single) {
+        acc_p = cp;
+      } else {
+        fold_part(acc_p, cp);
       }
       wave_lds_fence();  // the chunk's LDS reads are done before the next chunk's DMA
     }
-    fold_part(acc_p, first_part);
+    if (nparts > kStageParts) fold_part(acc_p, first_part);
     if (!ok) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
