@@ -658,56 +658,80 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
     }
   }
   // The last part of a cut sequence: wait for the other parts' flags, fold them in span
-  // order and this bin's part last, write the rows, lower the flags.
+  // order and this bin's part last, write the rows, lower the flags. This code stays small
+  // and its loops rolled: it runs once per merge, cold in the instruction cache, where every
+  // 64-byte line fetched costs an L2 round trip.
   if (complete && nspan0 > 1 && kidx0 == nspan0 - 1 && slots_ok(slot0, nspan0) &&
       k00 + static_cast<int64_t>(kGroups) * kidx0 == static_cast<int64_t>(blockIdx.x) && k00 >= 0) {
     const int want = 1 + ((xcc_id() + 1) << 8);
     const int nparts = nspan0 - 1;  // parts 0 .. nspan0 - 2 are in the workspace
-    // The flags: lane k polls part base + k's (lanes past the span repeat the last part's),
-    // 64 per load, until all are raised.
     bool ok = true;
-    for (int base = 0; base < nparts; base += 64) {
-      const int32_t* flag =
-          reinterpret_cast<const int32_t*>(part_slot(slots, slot0, min(base + lane, nparts - 1), h) + kFlagOffset);
-      int f = 0;
-#pragma nounroll
-      for (int spins = 0; spins < kMaxSpins; ++spins) {
-        f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (__builtin_amdgcn_ballot_w64(f == 0) == 0) break;
-        __builtin_amdgcn_s_sleep(2);
-      }
-      // never raised, or raised on another XCD (its partial is not visible here)
-      if (__builtin_amdgcn_ballot_w64(f != want) != 0) ok = false;
-    }
-    // The partials, kStageParts per round trip, staged in the wave's LDS (free after the
-    // stream) by DMA and folded in span order. The loops stay rolled: this code runs once
-    // per merge, cold in the instruction cache, where every 64-byte line fetched costs an
-    // L2 round trip.
     Part acc_p;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      acc_p.m[r] = -INFINITY;
-      acc_p.l[r] = 0.f;
-      acc_p.o[0][r] = 0.f;
-      acc_p.o[1][r] = 0.f;
-    }
-    for (int c0 = 0; c0 < nparts; c0 += kStageParts) {
-      const int cn = min(kStageParts, nparts - c0);
+    if (nparts <= kStageParts) {
+      // One chunk: lane k polls part k's flag (lanes past the span repeat the last part's),
+      // and every part whose flag is up is staged right away, by DMA into its LDS slot
+      // (the wave's area is free after the stream), while the others are still awaited.
+      const int32_t* flag =
+          reinterpret_cast<const int32_t*>(part_slot(slots, slot0, min(lane, nparts - 1), h) + kFlagOffset);
+      uint64_t pending = (nparts == 64 ? ~0ull : (1ull << nparts) - 1);
+      int spins = 0;
 #pragma nounroll
-      for (int i = 0; i < cn; ++i) stage_part(part_slot(slots, slot0, c0 + i, h), lane, wl + i * kStageBytes);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      // A span of at most kStageParts earlier parts is one chunk, combined with this bin's
-      // own part; longer spans fold their chunks' results in order, then the own part.
-      const bool single = nparts <= kStageParts;
-      const Part cp = combine_staged(wl, cn, lane, first_part, single);
-      if (single) {
-        acc_p = cp;
-      } else {
-        fold_part(acc_p, cp);
+      while (pending != 0) {
+        const int f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // raised on another XCD: its partial is not visible here
+        if (__builtin_amdgcn_ballot_w64(lane < nparts && f != 0 && f != want) != 0) ok = false;
+        uint64_t ready = __builtin_amdgcn_ballot_w64(f != 0) & pending;
+        if (ready == 0) {
+          if (++spins >= kMaxSpins) {  // never raised: the rows become NaN
+            ok = false;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+          continue;
+        }
+        pending &= ~ready;
+#pragma nounroll
+        while (ready != 0) {
+          const int k = __builtin_ctzll(ready);
+          ready &= ready - 1;
+          stage_part(part_slot(slots, slot0, k, h), lane, wl + k * kStageBytes);
+        }
       }
-      wave_lds_fence();  // the chunk's LDS reads are done before the next chunk's DMA
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      acc_p = combine_staged(wl, nparts, lane, first_part, true);
+    } else {
+      // Longer spans: the flags, 64 per load, until all are raised; then the partials,
+      // kStageParts per round trip, each chunk combined and folded in span order, and the
+      // own part last.
+      for (int base = 0; base < nparts; base += 64) {
+        const int32_t* flag =
+            reinterpret_cast<const int32_t*>(part_slot(slots, slot0, min(base + lane, nparts - 1), h) + kFlagOffset);
+        int f = 0;
+#pragma nounroll
+        for (int spins = 0; spins < kMaxSpins; ++spins) {
+          f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (__builtin_amdgcn_ballot_w64(f == 0) == 0) break;
+          __builtin_amdgcn_s_sleep(2);
+        }
+        if (__builtin_amdgcn_ballot_w64(f != want) != 0) ok = false;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        acc_p.m[r] = -INFINITY;
+        acc_p.l[r] = 0.f;
+        acc_p.o[0][r] = 0.f;
+        acc_p.o[1][r] = 0.f;
+      }
+      for (int c0 = 0; c0 < nparts; c0 += kStageParts) {
+        const int cn = min(kStageParts, nparts - c0);
+#pragma nounroll
+        for (int i = 0; i < cn; ++i) stage_part(part_slot(slots, slot0, c0 + i, h), lane, wl + i * kStageBytes);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        fold_part(acc_p, combine_staged(wl, cn, lane, first_part, false));
+        wave_lds_fence();  // the chunk's LDS reads are done before the next chunk's DMA
+      }
+      fold_part(acc_p, first_part);
     }
-    if (nparts > kStageParts) fold_part(acc_p, first_part);
     if (!ok) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
