@@ -706,3 +706,70 @@ def test_bad_block_in_a_cut_sequence_poisons_only_its_row(device, where):
     assert torch.equal(bad[others], good[others])
     assert not torch.isnan(good).any()
     assert _flags_clear(workspace)
+
+
+def _spans(plan):
+    """{sequence: {part: (row, segment index, first block, blocks, parts)}} of a plan's cut
+    sequences."""
+    spans = {}
+    for r in range(plan.shape[0]):
+        for s in range(int(plan[r, 0])):
+            b, _, j0, n, _, kidx, nspan, _ = (int(v) for v in plan[r, 8 + 8 * s : 16 + 8 * s])
+            if nspan > 1:
+                spans.setdefault(b, {})[kidx] = (r, s, j0, n, nspan)
+    return spans
+
+
+@pytest.mark.parametrize("fault", ["missing earlier part", "slots outside the workspace", "sequence outside the batch"])
+def test_malformed_plans_stay_in_bounds_and_spoil_only_their_rows(device, fault):
+    """Plans that do not match the batch: a cut sequence whose earlier part's row was
+    dropped (its merge waits out its bounded spin and writes NaN), a cut sequence whose
+    partial slots point past the workspace (neither stored nor merged: its row is left
+    alone), a complete sequence relabelled past the batch (not written). Every other row
+    keeps the bits of the intact plan, and the part flags end at zero."""
+    w = workloads.batched_decode(batch=64, num_blocks=8192, seed=86)
+    plan = _hip.decode_plan(w.lengths, w.tables)
+    spans = _spans(plan)
+    assert spans
+    pool = _random_pool(device, w.num_blocks, 22)
+    queries = torch.from_numpy(w.queries(8)).to(device)
+    lens = torch.from_numpy(w.lengths).to(device)
+    tables = torch.from_numpy(w.tables).to(device)
+    workspace = torch.zeros(_hip.workspace_bytes(w.batch, w.tables.shape[1]), dtype=torch.uint8, device=device)
+    good = torch.full_like(queries, 7.0)
+    _hip.paged_decode_attention(good, queries, pool, 8, tables, lens, workspace=workspace)
+    bad_plan = plan.copy()
+    if fault == "missing earlier part":
+        b = min(spans)
+        row = spans[b][0][0]
+        bad_plan[row] = 0  # the whole bin is dropped: every sequence it touches is spoiled
+        spoiled = {int(x) for x in plan[row, 8 : 8 + 8 * int(plan[row, 0]) : 8]}
+        nan_rows = {x for x in spoiled if x in spans}
+    elif fault == "slots outside the workspace":
+        b = min(spans)
+        for row, s, _, _, _ in spans[b].values():
+            bad_plan[row, 8 + 8 * s + 7] = 1 << 30
+        spoiled, nan_rows = {b}, set()
+    else:
+        complete = [int(plan[r, 8 + 8 * s]) for r in range(plan.shape[0]) for s in range(int(plan[r, 0]))
+                    if plan[r, 8 + 8 * s + 6] == 1]
+        assert complete, "the workload has no sequence complete within one bin"
+        b = complete[0]
+        for r in range(plan.shape[0]):
+            for s in range(int(plan[r, 0])):
+                if plan[r, 8 + 8 * s] == b:
+                    bad_plan[r, 8 + 8 * s] = w.batch + 5
+        spoiled, nan_rows = {b}, set()
+    _say("malformed plan:", fault, "spoiled rows", sorted(spoiled))
+    bad = torch.full_like(queries, 7.0)
+    _hip.paged_decode_attention(bad, queries, pool, 8, tables, lens, plan=torch.from_numpy(bad_plan).to(device),
+                                workspace=workspace)
+    torch.cuda.synchronize()
+    others = [x for x in range(w.batch) if x not in spoiled]
+    assert torch.equal(bad[others], good[others])
+    for x in nan_rows:
+        assert torch.isnan(bad[x]).all(), x
+    if fault != "missing earlier part":
+        for x in spoiled:
+            assert torch.equal(bad[x], torch.full_like(bad[x], 7.0)), x  # never written
+    assert _flags_clear(workspace)
