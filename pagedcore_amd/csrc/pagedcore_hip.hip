@@ -179,7 +179,8 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_word_kernel(
 // workgroup j to XCD (j + s) mod 8 for one s per launch, so all bins of one sequence run on
 // one XCD and share its L2. A bin holds at most kMaxSegs sequences (segments) and
 // kMaxUnits blocks; a sequence longer than the rest of a bin continues in the group's next
-// bin(s) (a cut sequence, spanning nspan bins).
+// bin(s) (a cut sequence, spanning nspan bins). A bin that starts with the last part of a
+// cut sequence merges the others after its stream and is given a few blocks fewer.
 //
 // Each of the four waves streams one kv head's K and V of the bin's blocks, in bin order,
 // through a two-unit LDS ring filled by LDS DMA (global_load_lds_dwordx4, non-temporal: the
@@ -206,8 +207,9 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_word_kernel(
 // sequence leaves one fp32 partial per bin and kv head in the workspace: every part but the
 // last is stored by its bin, which then raises the part's flag (after the stores are
 // acknowledged); the bin holding the last part (dispatched after all the others, so waiting
-// cannot deadlock) waits for the flags, folds the parts in span order with its own last,
-// writes the output and lowers the flags. Partials and flags stay in the XCD's L2 (plain
+// cannot deadlock) stages each part in LDS as its flag rises, combines them in span order
+// with its own last (their max first, then the weighted sums), writes the output and lowers
+// the flags. Partials and flags stay in the XCD's L2 (plain
 // stores and loads are coherent there); the flag carries the writer's XCD id and a merge
 // that sees another XCD's id writes NaN rows instead of reading stale partials.
 // ---------------------------------------------------------------------------------------
