@@ -1,8 +1,8 @@
 """The build's kernel resource check (CPU only: hipcc cross-compiles for gfx950 here).
 
-The attention item kernel's K loads are untracked inline assembly with hand-counted
-`vmcnt` waits, correct only while no register with a load in flight is spilled, copied or
-reused. The build therefore fails when a guarded kernel reports scratch, spills or fewer
+The decode attention kernel's LDS reads and DMA ring are untracked inline assembly with
+hand-counted `vmcnt` waits, correct only while no register with a load in flight is
+spilled, copied or reused. The build therefore fails when a guarded kernel reports scratch, spills or fewer
 waves per SIMD than its launch shape assumes; these tests show that a spilling build is
 refused and the shipped kernels pass."""
 
