@@ -237,8 +237,10 @@ def cpu_long_context_baseline(pool: Tensor, queries: Tensor, new_kv: Tensor, w: 
 def run_long_context(steps: int, warmup: int, cpu_seconds: float = 0.0) -> dict:
     """Long-context, high-occupancy decode: batch 256, every sequence at 2047 cached tokens
     (128 blocks), a fully shuffled 40000-block pool, 22 layers. Per layer the step appends
-    each sequence's new token (pc_kv_append, slot 2047) and then runs attention over 2048
-    tokens (split-K items + merge); both are timed together, replayed as one graph."""
+    each sequence's new token (slot 2047) and runs attention over 2048 tokens, replayed as
+    one graph: timed as one fused launch (pc_kv_append_paged_decode_attn) and, for
+    comparison, as the pair pc_kv_append + pc_paged_decode_attn. The two give the same bits
+    (checked here)."""
     device = torch.device("cuda:0")
     w = workloads.batched_decode(batch=256, num_blocks=40000, fixed_length=2048, seed=20261204)
     gen = torch.Generator(device=device).manual_seed(4321)
@@ -254,7 +256,7 @@ def run_long_context(steps: int, warmup: int, cpu_seconds: float = 0.0) -> dict:
     slots = torch.from_numpy(w.tables[:, max_blocks - 1].astype(np.int64) * 16 + 15).to(device)
     assert int(slots.max()) < w.num_blocks * 16
 
-    def step() -> None:
+    def pair_step() -> None:
         stream = torch.cuda.current_stream(device).cuda_stream
         for layer in range(LAYERS):
             status = lib.pc_kv_append(
@@ -268,28 +270,48 @@ def run_long_context(steps: int, warmup: int, cpu_seconds: float = 0.0) -> dict:
             if status:
                 raise RuntimeError(lib.pc_last_error().decode())
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize(device)
-    eager_out = out.clone()
-    graph = _captured(step, device)
-    graph.replay()
-    torch.cuda.synchronize(device)
-    if not torch.equal(out, eager_out):
-        raise RuntimeError("graph replay differs from eager launches")
-    total_ms = _timed(graph.replay, steps, device)
+    def fused_step() -> None:
+        stream = torch.cuda.current_stream(device).cuda_stream
+        for layer in range(LAYERS):
+            status = lib.pc_kv_append_paged_decode_attn(
+                out[layer].data_ptr(), queries[layer].data_ptr(), pool.data_ptr(), w.num_blocks, layer,
+                lens.data_ptr(), w.batch, max_blocks, plan.data_ptr(), plan.shape[0], new_kv[0, layer].data_ptr(),
+                new_kv[1, layer].data_ptr(), workspace.data_ptr(), stream,
+            )
+            if status:
+                raise RuntimeError(lib.pc_last_error().decode())
+
+    timings, outputs = {}, {}
+    for name, step in (("pair", pair_step), ("fused", fused_step)):
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize(device)
+        eager_out = out.clone()
+        graph = _captured(step, device)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        if not torch.equal(out, eager_out):
+            raise RuntimeError(f"{name}: graph replay differs from eager launches")
+        outputs[name] = eager_out
+        timings[name] = _timed(graph.replay, steps, device)
+        del graph
+    if not torch.equal(outputs["pair"].view(torch.int16), outputs["fused"].view(torch.int16)):
+        raise RuntimeError("fused append + attention differs from pc_kv_append + pc_paged_decode_attn")
+    total_ms = timings["fused"]
     attn = attention_bytes(w.lengths)
     append = w.batch * 1024 * 2  # read the new K/V rows, write them to their slots
     per_step = (attn + append) * LAYERS
     result = {
         "workload": "batch 256, every sequence 2047 cached + 1 appended (128 blocks), 40000-block shuffled pool, "
-        "22 layers; per layer pc_kv_append of the 256 new tokens + pc_paged_decode_attn, replayed as one graph",
+        "22 layers; per layer one pc_kv_append_paged_decode_attn (append of the 256 new tokens fused with "
+        "attention), replayed as one graph",
         "ms_per_step": round(total_ms / steps, 4),
         "gbps": round(per_step * steps / (total_ms / 1e3) / 1e9, 2),
         "hbm_fraction": round(per_step * steps / (total_ms / 1e3) / 1e9 / PEAK_HBM_GBPS, 4),
         "decode_tokens_per_s": round(w.batch * steps / (total_ms / 1e3), 1),
         "bytes_per_layer": attn + append,
         "us_per_layer": round(total_ms / steps / LAYERS * 1e3, 3),
+        "unfused_us_per_layer": round(timings["pair"] / steps / LAYERS * 1e3, 3),
     }
     if cpu_seconds > 0:
         result["cpu_baseline"] = cpu_long_context_baseline(pool, queries, new_kv, w, cpu_seconds)

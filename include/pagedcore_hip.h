@@ -97,6 +97,32 @@ int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t
                          const int32_t* context_lens, int32_t batch, int32_t max_blocks, const int32_t* plan,
                          int32_t num_records, void* workspace, void* stream);
 
+/*
+ * KV append of each sequence's newest token fused with paged decode attention over it.
+ *
+ * Replaces the decode step's KVAllocator.write_decode_layer row copies followed by
+ * paged_attention (reference src/pagedcore/decoder.py:187-190, kv_cache.py:221-246,
+ * attention.py:14-53) when the key and value are already projected: one launch instead of
+ * pc_kv_append + pc_paged_decode_attn, with the same results.
+ *
+ *   new_key, new_value  [batch][4][64] fp16, contiguous, 16-byte aligned: the token at
+ *                       position context_lens[b] - 1 of sequence b
+ *   other arguments     as pc_paged_decode_attn (pool writable)
+ *
+ * For each sequence b of the plan with length n > 0, the rows go to
+ * pool[layer][0 / 1][table[b][(n - 1) / 16]][(n - 1) % 16] (the table as carried by the
+ * plan; a block id outside [0, num_blocks) is not written, and its sequence's output rows
+ * become NaN as in pc_paged_decode_attn), then out is what pc_paged_decode_attn gives on the
+ * updated pool: bit-identical to pc_kv_append of those slots followed by
+ * pc_paged_decode_attn. The block a new token goes into must not be read by another
+ * sequence of the batch (a block taking new tokens belongs to one sequence); other layers
+ * and other rows of the pool are not touched.
+ */
+int pc_kv_append_paged_decode_attn(void* out, const void* query, void* pool, int64_t num_blocks, int32_t layer,
+                                   const int32_t* context_lens, int32_t batch, int32_t max_blocks,
+                                   const int32_t* plan, int32_t num_records, const void* new_key,
+                                   const void* new_value, void* workspace, void* stream);
+
 /* Workspace size in bytes for pc_paged_decode_attn; 0 on invalid arguments. */
 int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks);
 

@@ -17,7 +17,7 @@ import numpy as np
 import torch
 from torch import Tensor
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 LIBRARY_NAME = "libpagedcore_hip.so"
 
 _lock = threading.Lock()
@@ -47,6 +47,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pc_kv_append.argtypes = [_p, _i64, _i32, _i32, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _p]
     lib.pc_paged_decode_attn.restype = ctypes.c_int
     lib.pc_paged_decode_attn.argtypes = [_p, _p, _p, _i64, _i32, _p, _i32, _i32, _p, _i32, _p, _p]
+    lib.pc_kv_append_paged_decode_attn.restype = ctypes.c_int
+    lib.pc_kv_append_paged_decode_attn.argtypes = [_p, _p, _p, _i64, _i32, _p, _i32, _i32, _p, _i32, _p, _p, _p, _p]
     lib.pc_paged_decode_attn_noalloc.restype = ctypes.c_int
     lib.pc_paged_decode_attn_noalloc.argtypes = [_p, _p, _p, _i64, _i32, _p, _i32, _i32, _p, _i32, _p]
     lib.pc_attn_plan.restype = _i32
@@ -260,12 +262,17 @@ def paged_decode_attention(
 
 def planned_decode_attention(
     out: Tensor, query: Tensor, pool: Tensor, layer: int, context_lens: Tensor, plan: Tensor, max_blocks: int,
-    workspace: Tensor,
+    workspace: Tensor, *, new_key: Optional[Tensor] = None, new_value: Optional[Tensor] = None,
 ) -> None:
     """pc_paged_decode_attn with a ready device plan (decode_plan() rows, possibly padded
     with empty rows) for a batch of context_lens.shape[0] rows whose tables are at most
     max_blocks wide; workspace of workspace_bytes(batch, max_blocks) bytes, zero before its
-    first use (every call leaves it so)."""
+    first use (every call leaves it so).
+
+    With new_key and new_value (fp16 [batch, 4, 64] contiguous, the token at position
+    context_lens[b] - 1 of each sequence) the call is pc_kv_append_paged_decode_attn: the
+    rows are appended to layer `layer` of the pool in the same launch, with the results of
+    kv_append followed by attention."""
     lib = load()
     batch = int(context_lens.shape[0])
     nbytes = int(lib.pc_attn_workspace_bytes(batch, max_blocks))
@@ -280,21 +287,25 @@ def planned_decode_attention(
         or not plan.is_contiguous()
     ):
         raise HipExtensionError("plan must be a contiguous int32 decode_plan() array")
-    status = lib.pc_paged_decode_attn(
-        out.data_ptr(),
-        query.data_ptr(),
-        pool.data_ptr(),
-        pool.shape[2],
-        layer,
-        context_lens.data_ptr(),
-        batch,
-        max_blocks,
-        plan.data_ptr(),
-        int(plan.shape[0]),
-        workspace.data_ptr(),
-        _stream(pool.device),
+    args = (out.data_ptr(), query.data_ptr(), pool.data_ptr(), pool.shape[2], layer, context_lens.data_ptr(), batch,
+            max_blocks, plan.data_ptr(), int(plan.shape[0]))
+    if new_key is None and new_value is None:
+        status = lib.pc_paged_decode_attn(*args, workspace.data_ptr(), _stream(pool.device))
+        _check(lib, "pc_paged_decode_attn", status)
+        return
+    for name, rows in (("new_key", new_key), ("new_value", new_value)):
+        if (
+            rows is None
+            or rows.dtype != torch.float16
+            or tuple(rows.shape) != (batch, 4, 64)
+            or not rows.is_contiguous()
+            or rows.device != pool.device
+        ):
+            raise HipExtensionError(f"{name} must be a contiguous fp16 [{batch}, 4, 64] tensor on the pool's device")
+    status = lib.pc_kv_append_paged_decode_attn(
+        *args, new_key.data_ptr(), new_value.data_ptr(), workspace.data_ptr(), _stream(pool.device)
     )
-    _check(lib, "pc_paged_decode_attn", status)
+    _check(lib, "pc_kv_append_paged_decode_attn", status)
 
 
 def _ptr(tensor: Optional[Tensor]) -> Optional[int]:

@@ -62,7 +62,7 @@ using pc_internal::check_launch;
 using pc_internal::ok;
 using pc_internal::set_error;
 
-constexpr int kAbiVersion = 11;
+constexpr int kAbiVersion = 12;
 constexpr int kLayers = 22;
 constexpr int kSlots = 16;
 constexpr int kKVHeads = 4;
@@ -249,7 +249,8 @@ __device__ __forceinline__ int xcc_id() {
 }
 
 // The ring's unit u has landed: at most `later` units (4 DMAs each) issued after it may be
-// outstanding. Loads return in order; no store is issued while the ring runs.
+// outstanding. Loads return in order; a store among them (the fused append's, one per
+// sequence) only raises the count, so the wait never ends before unit u has landed.
 __device__ __forceinline__ void wait_ring(int later) {
   if (later > 0) {
     asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
@@ -419,10 +420,18 @@ __device__ __forceinline__ char* part_slot(char* slots, int first, int k, int h)
 
 // Scalar parameters in an order whose leading ones (plan, query, pool, num_blocks, layer)
 // the compiler preloads into SGPRs at wave launch.
+//
+// APPEND: the newest token of each sequence (position length - 1), given as new_key and
+// new_value [batch][4][64], is written into the pool row its block table gives. The bin
+// holding the sequence's last block stages the row in LDS with the Q DMAs, and once that
+// block's DMA has landed copies the row into its ring slot (so this pass already reads it)
+// and stores it to the pool.
+template <bool APPEND>
 __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int32_t* plan, const _Float16* query,
-                                                                      const _Float16* pool, int64_t num_blocks,
+                                                                      _Float16* pool, int64_t num_blocks,
                                                                       int layer, int batch, int nslots, _Float16* out,
-                                                                      char* slots) {
+                                                                      char* slots, const _Float16* new_key,
+                                                                      const _Float16* new_value) {
   __shared__ __attribute__((aligned(16))) char lds[kKVHeads * kWaveLds];
   const int h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -461,6 +470,20 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), lds_ptr(qarea + s * 1024), 16, 0, 0);
     }
   }
+  // APPEND: the new K row (lane L < 8: 16 B chunk L) and V row (lanes 8-15: chunk L - 8) of
+  // this wave's kv head into the segment's output area (unused until the segment ends);
+  // lanes 16-63 repeat lanes 0-15. Issued before the ring, so the first ring wait covers them.
+  if constexpr (APPEND) {
+#pragma unroll
+    for (int s = 0; s < kMaxSegs; ++s) {
+      if (s < nseg) {
+        int b = rec[kHeaderInts + s * kSegInts];
+        b = (b < 0 || b >= batch) ? 0 : b;
+        const _Float16* src = (c < 8 ? new_key : new_value) + (static_cast<int64_t>(b) * kKVHeads + h) * kHeadDim + 8 * (c & 7);
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), lds_ptr(oarea + s * 1024), 16, 0, 0);
+      }
+    }
+  }
   auto block_id = [&](int u) -> uint32_t {
     const int32_t v = u < 64 ? idv[0] : u < 128 ? idv[1] : u < 192 ? idv[2] : idv[3];
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(v, u & 63));
@@ -494,6 +517,7 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
   const uint32_t ring_base = lds_offset(ring);
 
   Part first_part, last_part;  // partials of segment 0 and of the last segment (cut sequences)
+  int patch_u = -1;  // APPEND: the segment's unit holding the new token, or -1
   int seg = -1, seg_end = 0, len = 0, j0 = 0, nblk = 0, nspan = 1;
   half8_t qa, qb;
   float m = 0.f, mc = 0.f, lsum = 0.f;
@@ -530,6 +554,11 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
       nblk = seg == 0 ? rec[11] : seg == 1 ? rec[19] : seg == 2 ? rec[27] : rec[35];
       nspan = seg == 0 ? rec[14] : seg == 1 ? rec[22] : seg == 2 ? rec[30] : rec[38];
       seg_end = u + max(nblk, 1);
+      if constexpr (APPEND) {
+        const int sb = seg == 0 ? rec[8] : seg == 1 ? rec[16] : seg == 2 ? rec[24] : rec[32];
+        const bool ends = nblk > 0 && len > 0 && j0 + nblk == blocks_of(len) && sb >= 0 && sb < batch;
+        patch_u = ends ? seg_end - 1 : -1;
+      }
       bad = false;
       first_block = true;
       lsum = 0.f;
@@ -537,6 +566,36 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
       for (int nt = 0; nt < 4; ++nt) acc[nt] = float4_t{0.f, 0.f, 0.f, 0.f};
     }
     wait_ring(issued - u - 1);  // also covers the Q DMAs, issued before every unit
+    if constexpr (APPEND) {
+      if (u == patch_u) {
+        // The block holding the new token has landed: its staged row replaces the pool's
+        // (stale) row in the ring slot (K chunk c at c ^ (r & 7), V chunk c at
+        // 2 ((c / 2) ^ row_sel(r)) + c % 2 of row r) and goes to the pool, K by lanes 0-7, V
+        // by lanes 8-15. LDS accesses as assembly, so the compiler adds no wait for the ring's
+        // DMAs still in flight; the one store only lengthens later ring waits (loads return
+        // in order, so an extra count never lets a wait end early).
+        const int r = (len - 1) % kSlots, ch = c & 7;
+        const int pos = c < 8 ? (ch ^ (r & 7)) : 128 + 2 * ((ch >> 1) ^ row_sel(r)) + (ch & 1);
+        half8_t v;
+        asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                     : "=v"(v)
+                     : "v"(lds_offset(oarea + seg * 1024 + c * 16))
+                     : "memory");
+        // The id is read with every lane active: block_id selects its vector per lane, and
+        // readlane of a lane outside a branch's exec mask would see a stale register.
+        const uint32_t id = block_id(u);
+        if (lane < 16) {
+          asm volatile("ds_write_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                       :
+                       : "v"(ring_base + (u & (kRing - 1)) * kUnitBytes + r * 128 + pos * 16), "v"(v)
+                       : "memory");
+          if (id < static_cast<uint64_t>(num_blocks)) {
+            *reinterpret_cast<half8_t*>(pool + ((static_cast<int64_t>(layer) * 2 + (c >> 3)) * num_blocks + id) *
+                                                   kBlockElems + r * kRowElems + h * kHeadDim + 8 * ch) = v;
+          }
+        }
+      }
+    }
     if (first_block) {
       const uint32_t qbase = lds_offset(qarea + seg * 1024);
       asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
@@ -821,6 +880,36 @@ void* scratch_address(int device) {
   return g_scratch_ptr[device];
 }
 
+// Argument checks and the launch of pc_paged_decode_attn (APPEND false) and
+// pc_kv_append_paged_decode_attn (APPEND true, new_key and new_value checked by the caller).
+template <bool APPEND>
+int launch_decode_attn(void* out, const void* query, void* pool, int64_t num_blocks, int32_t layer,
+                       const int32_t* context_lens, int32_t batch, int32_t max_blocks, const int32_t* plan,
+                       int32_t num_records, const void* new_key, const void* new_value, void* workspace,
+                       void* stream) {
+  if (!out || !query || !pool || !context_lens || !plan) return set_error(PC_ERR_ARGUMENT, "null pointer");
+  if (!workspace) return set_error(PC_ERR_ARGUMENT, "workspace required (null pointer)");
+  if (num_blocks < 1 || num_blocks > INT32_MAX) return set_error(PC_ERR_ARGUMENT, "num_blocks out of range");
+  if (layer < 0 || layer >= kLayers) return set_error(PC_ERR_ARGUMENT, "layer %d outside [0, 22)", layer);
+  if (int rc = check_attn_shape(batch, max_blocks)) return rc;
+  if (!aligned(query, 16) || !aligned(out, 16) || !aligned(pool, 16) || !aligned(workspace, 256) ||
+      !aligned(plan, 16) || !aligned(context_lens, 4)) {
+    return set_error(PC_ERR_ARGUMENT, "query/out/pool/plan must be 16-byte, workspace 256-byte aligned");
+  }
+  if (num_records < 0 || num_records > plan_rows_bound(batch, max_blocks)) {
+    return set_error(PC_ERR_ARGUMENT, "num_records %d outside [0, pc_attn_plan_capacity]", num_records);
+  }
+  const int64_t nslots = slots_bound(batch, max_blocks);
+  if (batch == 0 || num_records == 0) return ok();
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(paged_decode_bin_kernel<APPEND>, dim3(static_cast<unsigned>(num_records)), dim3(kBinThreads), 0, s,
+                     plan, static_cast<const _Float16*>(query), static_cast<_Float16*>(pool), num_blocks, layer, batch,
+                     static_cast<int>(nslots), static_cast<_Float16*>(out), static_cast<char*>(workspace),
+                     static_cast<const _Float16*>(new_key), static_cast<const _Float16*>(new_value));
+  return check_launch(APPEND ? "kv_append_paged_decode_bin" : "paged_decode_bin");
+}
+
 // One bin while it is being cut: its segments {sequence, first block, blocks}.
 struct BinSegs {
   int32_t seg[kMaxSegs][3];
@@ -1032,26 +1121,20 @@ int pc_kv_append(void* pool, int64_t num_blocks, int32_t layer_begin, int32_t nu
 int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t num_blocks, int32_t layer,
                          const int32_t* context_lens, int32_t batch, int32_t max_blocks, const int32_t* plan,
                          int32_t num_records, void* workspace, void* stream) {
-  if (!out || !query || !pool || !context_lens || !plan) return set_error(PC_ERR_ARGUMENT, "null pointer");
-  if (!workspace) return set_error(PC_ERR_ARGUMENT, "workspace required (null pointer)");
-  if (num_blocks < 1 || num_blocks > INT32_MAX) return set_error(PC_ERR_ARGUMENT, "num_blocks out of range");
-  if (layer < 0 || layer >= kLayers) return set_error(PC_ERR_ARGUMENT, "layer %d outside [0, 22)", layer);
-  if (int rc = check_attn_shape(batch, max_blocks)) return rc;
-  if (!aligned(query, 16) || !aligned(out, 16) || !aligned(pool, 16) || !aligned(workspace, 256) ||
-      !aligned(plan, 16) || !aligned(context_lens, 4)) {
-    return set_error(PC_ERR_ARGUMENT, "query/out/pool/plan must be 16-byte, workspace 256-byte aligned");
+  return launch_decode_attn<false>(out, query, const_cast<void*>(pool), num_blocks, layer, context_lens, batch,
+                                   max_blocks, plan, num_records, nullptr, nullptr, workspace, stream);
+}
+
+int pc_kv_append_paged_decode_attn(void* out, const void* query, void* pool, int64_t num_blocks, int32_t layer,
+                                   const int32_t* context_lens, int32_t batch, int32_t max_blocks,
+                                   const int32_t* plan, int32_t num_records, const void* new_key,
+                                   const void* new_value, void* workspace, void* stream) {
+  if (!new_key || !new_value) return set_error(PC_ERR_ARGUMENT, "null pointer");
+  if (!aligned(new_key, 16) || !aligned(new_value, 16)) {
+    return set_error(PC_ERR_ARGUMENT, "new_key/new_value must be 16-byte aligned");
   }
-  if (num_records < 0 || num_records > plan_rows_bound(batch, max_blocks)) {
-    return set_error(PC_ERR_ARGUMENT, "num_records %d outside [0, pc_attn_plan_capacity]", num_records);
-  }
-  const int64_t nslots = slots_bound(batch, max_blocks);
-  if (batch == 0 || num_records == 0) return ok();
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  (void)hipGetLastError();
-  hipLaunchKernelGGL(paged_decode_bin_kernel, dim3(static_cast<unsigned>(num_records)), dim3(kBinThreads), 0, s, plan,
-                     static_cast<const _Float16*>(query), static_cast<const _Float16*>(pool), num_blocks, layer, batch,
-                     static_cast<int>(nslots), static_cast<_Float16*>(out), static_cast<char*>(workspace));
-  return check_launch("paged_decode_bin");
+  return launch_decode_attn<true>(out, query, pool, num_blocks, layer, context_lens, batch, max_blocks, plan,
+                                  num_records, new_key, new_value, workspace, stream);
 }
 
 int pc_paged_decode_attn_noalloc(void* out, const void* query, const void* pool, int64_t num_blocks, int32_t layer,

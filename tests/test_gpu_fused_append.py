@@ -1,0 +1,227 @@
+"""pc_kv_append_paged_decode_attn on the GPU: one launch that appends each sequence's newest
+token and attends over it, against the two launches it replaces.
+
+The decode step of the reference writes the new key and value (KVAllocator.write_decode_layer,
+reference src/pagedcore/kv_cache.py:221-246) and then runs paged_attention over the history
+that now holds them (reference src/pagedcore/decoder.py:187-190). The fused call must give
+the same bits as pc_kv_append of those slots followed by pc_paged_decode_attn: the whole
+pool (every layer, every row) and every output row compared with torch.equal. The unfused
+pair is itself held to the oracle and to FP64 by the attention tests; one case here also
+checks the fused rows against FP64 directly, within the 2e-3 max-abs bound.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from pagedcore_amd import _hip
+from tests import workloads
+from tests.bin_plan import check_decode_plan, regrouped_plan
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+
+
+def _say(*parts) -> None:
+    print(*parts, flush=True)
+    sys.stdout.flush()
+
+
+def _tables(lengths, num_blocks, seed):
+    need = [(int(x) + 15) // 16 for x in lengths]
+    perm = np.random.default_rng(seed).permutation(num_blocks).astype(np.int32)
+    tables = np.zeros((len(lengths), max(max(need), 1)), dtype=np.int32)
+    offset = 0
+    for b, n in enumerate(need):
+        tables[b, :n] = perm[offset : offset + n]
+        offset += n
+    return tables
+
+
+def _slots(lengths, tables):
+    """The pool slot of each sequence's newest token (position length - 1), -1 for an empty
+    sequence: what pc_kv_append is given in the unfused pair."""
+    slots = np.full(len(lengths), -1, dtype=np.int64)
+    for b, n in enumerate(lengths):
+        if n > 0:
+            slots[b] = int(tables[b, (n - 1) // 16]) * 16 + (n - 1) % 16
+    return slots
+
+
+def _flags_clear(workspace) -> bool:
+    slots = workspace.numel() // 2176
+    return not workspace[: slots * 2176].view(slots, 2176)[:, 2112:2116].any().item()
+
+
+def _fp64_rows(pool, layer, tables, lengths, queries):
+    out = torch.empty((len(lengths), 32, 64), dtype=torch.float64)
+    for b, n in enumerate(lengths):
+        width = (int(n) + 15) // 16
+        ids = torch.as_tensor(tables[b, :width].astype(np.int64), device=pool.device)
+        k = pool[layer, 0].index_select(0, ids).cpu().reshape(width * 16, 4, 64)[:n].permute(1, 0, 2).double()
+        v = pool[layer, 1].index_select(0, ids).cpu().reshape(width * 16, 4, 64)[:n].permute(1, 0, 2).double()
+        q = queries[b].cpu().double().reshape(4, 8, 64)
+        scores = torch.matmul(q, k.transpose(-1, -2).contiguous()) / 8.0
+        out[b] = torch.matmul(torch.softmax(scores, dim=-1), v).reshape(32, 64)
+    return out
+
+
+def _both_ways(device, lengths, tables, num_blocks, layer, seed, plan=None, check_plan=True):
+    """(pool, out) of the unfused pair and of the fused call, from the same inputs, plus the
+    fused call's workspace and the queries. check_plan: the plan covers every block once
+    with ids inside the pool (off for tables that hold an id outside it on purpose)."""
+    lengths = np.asarray(lengths, dtype=np.int32)
+    batch = len(lengths)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    pool = torch.randn((22, 2, num_blocks, 16, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    queries = torch.randn((batch, 32, 64), dtype=torch.float16, device=device, generator=gen)
+    new_key = torch.randn((batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    new_value = torch.randn((batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    if plan is None:
+        plan = _hip.decode_plan(lengths, tables)
+    if check_plan:
+        check_decode_plan(plan, lengths, tables, num_blocks, _hip.workspace_bytes(batch, tables.shape[1]))
+    plan_d = torch.from_numpy(np.ascontiguousarray(plan)).to(device)
+    lens_d = torch.from_numpy(lengths).to(device)
+    nbytes = _hip.workspace_bytes(batch, tables.shape[1])
+
+    pool_a = pool.clone()
+    out_a = torch.full_like(queries, float("nan"))
+    ws_a = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    _hip.kv_append(pool_a, layer, new_key[None], new_value[None], torch.from_numpy(_slots(lengths, tables)).to(device))
+    _hip.planned_decode_attention(out_a, queries, pool_a, layer, lens_d, plan_d, tables.shape[1], ws_a)
+
+    pool_b = pool
+    out_b = torch.full_like(queries, float("nan"))
+    ws_b = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    _hip.planned_decode_attention(out_b, queries, pool_b, layer, lens_d, plan_d, tables.shape[1], ws_b,
+                                  new_key=new_key, new_value=new_value)
+    torch.cuda.synchronize()
+    return (pool_a, out_a), (pool_b, out_b), ws_b, queries
+
+
+def _where(x, y, dims):
+    """Count and the first few index tuples (over the leading `dims` axes) where x and y
+    differ bitwise."""
+    diff = (x.view(torch.int16) != y.view(torch.int16)).reshape(*x.shape[:dims], -1).any(-1)
+    at = diff.nonzero().tolist()
+    return len(at), at[:8]
+
+
+def _assert_same(a, b, what):
+    (pool_a, out_a), (pool_b, out_b) = a, b
+    count, first = _where(pool_a, pool_b, 5)
+    assert count == 0, f"{what}: pools differ at {count} (layer, kind, block, slot, head) rows, first {first}"
+    count, first = _where(out_a, out_b, 2)
+    assert count == 0, f"{what}: outputs differ at {count} (sequence, q head) rows, first {first}"
+
+
+CASES = {
+    # batch 64, lengths U{1..2048}: one to four sequences per bin, every last block patched
+    "batch 64": (lambda: workloads.batched_decode(batch=64, num_blocks=8192, seed=91), None),
+    # block boundaries: the new token at slot 0, 1, 14, 15 of its block, and empty rows
+    "block boundaries": ([0, 1, 2, 15, 16, 17, 31, 32, 33, 47, 48, 0, 1000, 2047, 2048], 600),
+    # sequences cut over many bins: the new token sits in the merging bin's last block
+    "cut sequences": ([20000, 1, 5000, 16, 17, 8191], 2400),
+    # 1000 short sequences: four segments per bin, each one ending at its sequence's last block
+    "many short": (None, 3000),
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_fused_append_matches_append_then_attention(device, case):
+    """Whole pool and every output row bit-identical to pc_kv_append + pc_paged_decode_attn;
+    the part flags end at zero."""
+    _say("fused append + attention:", case)
+    source, num_blocks = CASES[case]
+    if case == "batch 64":
+        w = source()
+        lengths, tables, num_blocks = w.lengths, w.tables, w.num_blocks
+    elif case == "many short":
+        lengths = np.random.default_rng(92).integers(1, 49, size=1000).astype(np.int32)
+        tables = _tables(lengths, num_blocks, 93)
+    else:
+        lengths = np.asarray(source, dtype=np.int32)
+        tables = _tables(lengths, num_blocks, 94)
+    a, b, workspace, queries = _both_ways(device, lengths, tables, num_blocks, layer=9, seed=95)
+    _assert_same(a, b, case)
+    assert _flags_clear(workspace)
+    nonempty = np.flatnonzero(np.asarray(lengths) > 0)
+    assert torch.isfinite(b[1][torch.from_numpy(nonempty).to(device)]).all()
+
+
+def test_fused_rows_match_fp64_after_append(device):
+    """The fused call's outputs against FP64 attention over the appended history (the new
+    token's row included), within 2e-3, for tokens on both sides of a block boundary."""
+    lengths = np.asarray([1, 15, 16, 17, 33, 500, 2048, 2047], dtype=np.int32)
+    tables = _tables(lengths, 400, 96)
+    _, (pool, out), _, queries = _both_ways(device, lengths, tables, 400, layer=21, seed=97)
+    expected = _fp64_rows(pool, 21, tables, lengths, queries)
+    error = (out.cpu().double() - expected).abs().max().item()
+    _say(f"fused rows vs fp64: max error {error:.2e}")
+    assert error <= ATOL
+
+
+def test_fused_append_with_regrouped_bins(device):
+    """The plan's groups of bins moved to other XCDs: the same bits as the unfused pair."""
+    w = workloads.batched_decode(batch=64, num_blocks=8192, seed=98)
+    plan = regrouped_plan(_hip.decode_plan(w.lengths, w.tables), np.random.default_rng(4).permutation(8))
+    a, b, workspace, _ = _both_ways(device, w.lengths, w.tables, w.num_blocks, layer=0, seed=99, plan=plan)
+    _assert_same(a, b, "regrouped")
+    assert _flags_clear(workspace)
+
+
+@pytest.mark.parametrize("where", ["last block", "earlier block"])
+def test_out_of_pool_block_id(device, where):
+    """An id outside the pool in a table: that row is NaN in both paths; in its last block
+    the new token is not written (pc_kv_append skips the slot too); elsewhere it is. Pools
+    and the other rows stay bit-identical."""
+    lengths = np.asarray([300, 40, 1000, 17], dtype=np.int32)
+    num_blocks = 200
+    tables = _tables(lengths, num_blocks, 100)
+    row = 2
+    col = (int(lengths[row]) - 1) // 16 if where == "last block" else 3
+    tables[row, col] = num_blocks + 5
+    a, b, _, _ = _both_ways(device, lengths, tables, num_blocks, layer=4, seed=101, check_plan=False)
+    assert torch.isnan(b[1][row]).all()
+    keep = [r for r in range(len(lengths)) if r != row]
+    assert torch.equal(a[1][keep].view(torch.int16), b[1][keep].view(torch.int16))
+    assert torch.equal(a[0].view(torch.int16), b[0].view(torch.int16))
+
+
+def test_fused_call_appends_in_place_over_a_decode_run(device):
+    """Five decode steps of one layer: each step's fused call appends at the next position
+    and attends; after the run the pool and the last outputs match five unfused steps."""
+    lengths0 = np.asarray([14, 31, 1, 250], dtype=np.int32)
+    num_blocks = 64
+    tables = _tables(lengths0 + 5, num_blocks, 102)
+    gen = torch.Generator(device=device).manual_seed(103)
+    pool0 = torch.randn((22, 2, num_blocks, 16, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    pools = {"fused": pool0.clone(), "pair": pool0.clone()}
+    outs = {}
+    nbytes = _hip.workspace_bytes(len(lengths0), tables.shape[1])
+    workspaces = {k: torch.zeros(nbytes, dtype=torch.uint8, device=device) for k in pools}
+    for step in range(5):
+        lengths = lengths0 + 1 + step
+        queries = torch.randn((4, 32, 64), dtype=torch.float16, device=device, generator=gen)
+        key = torch.randn((4, 4, 64), dtype=torch.float16, device=device, generator=gen)
+        value = torch.randn((4, 4, 64), dtype=torch.float16, device=device, generator=gen)
+        plan = torch.from_numpy(_hip.decode_plan(lengths, tables)).to(device)
+        lens = torch.from_numpy(lengths).to(device)
+        for kind, pool in pools.items():
+            out = torch.empty_like(queries)
+            if kind == "pair":
+                _hip.kv_append(pool, 6, key[None], value[None], torch.from_numpy(_slots(lengths, tables)).to(device))
+                _hip.planned_decode_attention(out, queries, pool, 6, lens, plan, tables.shape[1], workspaces[kind])
+            else:
+                _hip.planned_decode_attention(out, queries, pool, 6, lens, plan, tables.shape[1], workspaces[kind],
+                                              new_key=key, new_value=value)
+            outs[kind] = out
+        torch.cuda.synchronize()
+        assert torch.equal(outs["fused"].view(torch.int16), outs["pair"].view(torch.int16)), f"step {step}"
+    assert torch.equal(pools["fused"].view(torch.int16), pools["pair"].view(torch.int16))

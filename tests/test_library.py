@@ -103,6 +103,33 @@ def test_attention_rejects_invalid_arguments_without_a_gpu(overrides, needle):
     assert needle in lib.pc_last_error()
 
 
+@pytest.mark.parametrize(
+    "overrides,needle",
+    [
+        ({"key": None}, b"null pointer"),
+        ({"value": None}, b"null pointer"),
+        ({"key": 264}, b"new_key/new_value must be 16-byte aligned"),
+        ({"value": 258}, b"new_key/new_value must be 16-byte aligned"),
+        ({"layer": -1}, b"layer"),
+        ({"ws": None}, b"workspace"),
+        ({"nrec": 8 * (256 + 1 + 1 + 1) + 1}, b"num_records"),
+    ],
+)
+def test_fused_append_attention_rejects_invalid_arguments_without_a_gpu(overrides, needle):
+    """pc_kv_append_paged_decode_attn checks its rows, then everything pc_paged_decode_attn
+    checks, before any HIP call."""
+    lib = _hip.load()
+    a = {"out": 256, "query": 256, "pool": 256, "blocks": 10, "layer": 0, "lens": 256, "batch": 1,
+         "max_blocks": 128, "plan": 256, "nrec": 1, "key": 512, "value": 768, "ws": 256}
+    a.update(overrides)
+    status = lib.pc_kv_append_paged_decode_attn(
+        a["out"], a["query"], a["pool"], a["blocks"], a["layer"], a["lens"], a["batch"], a["max_blocks"],
+        a["plan"], a["nrec"], a["key"], a["value"], a["ws"], None,
+    )
+    assert status == 1
+    assert needle in lib.pc_last_error()
+
+
 def _plan_and_check(lengths, tables, num_blocks):
     lib = _hip.load()
     plan = _hip.decode_plan(lengths, tables)
