@@ -225,3 +225,42 @@ def test_fused_call_appends_in_place_over_a_decode_run(device):
         torch.cuda.synchronize()
         assert torch.equal(outs["fused"].view(torch.int16), outs["pair"].view(torch.int16)), f"step {step}"
     assert torch.equal(pools["fused"].view(torch.int16), pools["pair"].view(torch.int16))
+
+
+def test_fused_call_in_a_graph_replays_as_eager(device):
+    """The fused call captured in a HIP graph: three replays, with eager fused calls and
+    synchronizations between them, each give the eager call's pool and outputs."""
+    w = workloads.batched_decode(batch=32, num_blocks=4096, seed=104)
+    gen = torch.Generator(device=device).manual_seed(105)
+    pool = torch.randn((22, 2, w.num_blocks, 16, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    queries = torch.randn((w.batch, 32, 64), dtype=torch.float16, device=device, generator=gen)
+    key = torch.randn((w.batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    value = torch.randn((w.batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    plan = torch.from_numpy(_hip.decode_plan(w.lengths, w.tables)).to(device)
+    lens = torch.from_numpy(w.lengths).to(device)
+    width = w.tables.shape[1]
+    workspace = torch.zeros(_hip.workspace_bytes(w.batch, width), dtype=torch.uint8, device=device)
+    out = torch.empty_like(queries)
+
+    def call():
+        _hip.planned_decode_attention(out, queries, pool, 3, lens, plan, width, workspace, new_key=key, new_value=value)
+
+    call()
+    torch.cuda.synchronize()
+    eager_out, eager_pool = out.clone(), pool.clone()
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            call()
+    torch.cuda.current_stream(device).wait_stream(side)
+    for replay in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager_out.view(torch.int16)), f"replay {replay}"
+        assert torch.equal(pool.view(torch.int16), eager_pool.view(torch.int16)), f"replay {replay}"
+        assert _flags_clear(workspace)
+        call()  # eager work between replays
+        torch.cuda.synchronize()
