@@ -912,7 +912,7 @@ def main() -> int:
         "step_ms_max": round(r["step_ms_max"], 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "pc_paged_decode_attn: paged_decode_bin_kernel",
+            "kernel": "pc_paged_decode_attn: paged_decode_bin_kernel<false>",
             "achieved": round(r["launch_gbps"], 2),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
