@@ -264,3 +264,63 @@ def test_fused_call_in_a_graph_replays_as_eager(device):
         assert _flags_clear(workspace)
         call()  # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("fault", ["missing earlier part", "slots outside the workspace", "sequence outside the batch"])
+def test_fused_call_with_malformed_plans_writes_only_planned_rows(device, fault):
+    """The malformed plans of the attention tests, through the fused call: outputs of the
+    rows the fault does not touch keep the intact plan's bits, and the pool differs from
+    the intact plan's result at most in the new-token rows of the touched sequences, each
+    of which holds either its old bits or the new row (never anything else, nowhere else)."""
+    from tests.test_gpu_attention import _spans
+
+    w = workloads.batched_decode(batch=64, num_blocks=8192, seed=86)
+    plan = _hip.decode_plan(w.lengths, w.tables)
+    spans = _spans(plan)
+    bad_plan = plan.copy()
+    if fault == "missing earlier part":
+        row = spans[min(spans)][0][0]
+        bad_plan[row] = 0
+        spoiled = {int(x) for x in plan[row, 8 : 8 + 8 * int(plan[row, 0]) : 8]}
+    elif fault == "slots outside the workspace":
+        b = min(spans)
+        for row, s, _, _, _ in spans[b].values():
+            bad_plan[row, 8 + 8 * s + 7] = 1 << 30
+        spoiled = {b}
+    else:
+        b = next(int(plan[r, 8 + 8 * s]) for r in range(plan.shape[0]) for s in range(int(plan[r, 0]))
+                 if plan[r, 8 + 8 * s + 6] == 1)
+        for r in range(plan.shape[0]):
+            for s in range(int(plan[r, 0])):
+                if plan[r, 8 + 8 * s] == b:
+                    bad_plan[r, 8 + 8 * s] = w.batch + 5
+        spoiled = {b}
+    _say("fused call, malformed plan:", fault, "spoiled rows", sorted(spoiled))
+    gen = torch.Generator(device=device).manual_seed(106)
+    pool = torch.randn((22, 2, w.num_blocks, 16, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    queries = torch.randn((w.batch, 32, 64), dtype=torch.float16, device=device, generator=gen)
+    key = torch.randn((w.batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    value = torch.randn((w.batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    lens = torch.from_numpy(w.lengths).to(device)
+    width = w.tables.shape[1]
+    results = []
+    for p in (plan, bad_plan):
+        target = pool.clone()
+        out = torch.full_like(queries, 7.0)
+        workspace = torch.zeros(_hip.workspace_bytes(w.batch, width), dtype=torch.uint8, device=device)
+        _hip.planned_decode_attention(out, queries, target, 8, lens, torch.from_numpy(p).to(device), width, workspace,
+                                      new_key=key, new_value=value)
+        torch.cuda.synchronize()
+        assert _flags_clear(workspace)
+        results.append((target, out))
+    (good_pool, good), (bad_pool, bad) = results
+    others = [x for x in range(w.batch) if x not in spoiled]
+    assert torch.equal(bad[others].view(torch.int16), good[others].view(torch.int16))
+    slots = _slots(w.lengths, w.tables)
+    for x in sorted(spoiled):
+        block, offset = divmod(int(slots[x]), 16)
+        for kind, new in ((0, key[x]), (1, value[x])):
+            got = bad_pool[8, kind, block, offset].view(torch.int16)
+            assert torch.equal(got, new.view(torch.int16)) or torch.equal(got, pool[8, kind, block, offset].view(torch.int16))
+            bad_pool[8, kind, block, offset] = good_pool[8, kind, block, offset]
+    assert torch.equal(bad_pool.view(torch.int16), good_pool.view(torch.int16))
