@@ -1,7 +1,9 @@
-// Paged KV-cache hot path for MI355X (gfx950): KV append, paged decode attention over split-K
-// work items, and the merge of the items' partials. Exposed through the C ABI declared in
-// include/pagedcore_hip.h. No device memory is allocated here; every buffer comes from the
-// caller.
+// Paged KV-cache hot path for MI355X (gfx950): KV append; paged decode attention in balanced
+// bins, one workgroup each, with the split-K merge of a cut sequence's parts inside the same
+// kernel (optionally also appending each sequence's newest token); and the host planner
+// that cuts a batch into those bins. Exposed through the C ABI declared in
+// include/pagedcore_hip.h. No device memory is allocated at run time: every buffer comes from
+// the caller, except the fixed per-GPU split-K array of the allocation-free entry point.
 //
 // Pool layout (fixed by the reference allocator, src/pagedcore/kv_cache.py:39-43):
 //   fp16 [22 layers][2 kinds][num_blocks][16 slots][4 kv heads][64 dims]
