@@ -132,6 +132,7 @@ def run_decode(steps: int, warmup: int, use_graph: bool = True) -> dict:
     total_ms = start.elapsed_time(stop)
     if not torch.equal(layers.out, eager_out):
         raise RuntimeError("timed steps produced different outputs than the warmup")
+    _check_faults(layers.workspace, "attention")
     # A second, separate pass times each step alone (its own pair of events) for the median
     # the measurement plan asks for; `value` stays the whole timed region above.
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
@@ -175,6 +176,14 @@ def _timed(replay, steps: int, device: torch.device) -> float:
     stop.record()
     torch.cuda.synchronize(device)
     return start.elapsed_time(stop)
+
+
+def _check_faults(workspace: Tensor, where: str) -> None:
+    """Refuse to report a figure from runs whose attention recorded a device fault (a merge
+    that timed out or saw another XCD's flag, a block id outside the pool)."""
+    faults = int(_hip.fault_word(workspace).item())
+    if faults:
+        raise RuntimeError(f"{where}: paged attention recorded device fault word {faults:#x}")
 
 
 def _captured(fn, device: torch.device) -> torch.cuda.CUDAGraph:
@@ -239,12 +248,13 @@ def run_long_context(steps: int, warmup: int, cpu_seconds: float = 0.0) -> dict:
     (128 blocks), a fully shuffled 40000-block pool, 22 layers. Per layer the step appends
     each sequence's new token (slot 2047) and runs attention over 2048 tokens, replayed as
     one graph: timed as one fused launch (pc_kv_append_paged_decode_attn) and, for
-    comparison, as the pair pc_kv_append + pc_paged_decode_attn. The two give the same bits
-    (checked here)."""
+    comparison, as the pair pc_kv_append + pc_paged_decode_attn, each on its own copy of the
+    same pool. The two give the same bits (checked here): the outputs, and the whole pools
+    after every step either leg ran, so a new row stored anywhere but its slot shows."""
     device = torch.device("cuda:0")
     w = workloads.batched_decode(batch=256, num_blocks=40000, fixed_length=2048, seed=20261204)
     gen = torch.Generator(device=device).manual_seed(4321)
-    pool = torch.randn((LAYERS, 2, w.num_blocks, 16, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    base = torch.randn((LAYERS, 2, w.num_blocks, 16, 4, 64), dtype=torch.float16, device=device, generator=gen)
     queries = torch.randn((LAYERS, w.batch, 32, 64), dtype=torch.float16, device=device, generator=gen)
     new_kv = torch.randn((2, LAYERS, w.batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
     out = torch.empty_like(queries)
@@ -256,7 +266,10 @@ def run_long_context(steps: int, warmup: int, cpu_seconds: float = 0.0) -> dict:
     slots = torch.from_numpy(w.tables[:, max_blocks - 1].astype(np.int64) * 16 + 15).to(device)
     assert int(slots.max()) < w.num_blocks * 16
 
+    pools = {"pair": base.clone(), "fused": base}
+
     def pair_step() -> None:
+        pool = pools["pair"]
         stream = torch.cuda.current_stream(device).cuda_stream
         for layer in range(LAYERS):
             status = lib.pc_kv_append(
@@ -271,6 +284,7 @@ def run_long_context(steps: int, warmup: int, cpu_seconds: float = 0.0) -> dict:
                 raise RuntimeError(lib.pc_last_error().decode())
 
     def fused_step() -> None:
+        pool = pools["fused"]
         stream = torch.cuda.current_stream(device).cuda_stream
         for layer in range(LAYERS):
             status = lib.pc_kv_append_paged_decode_attn(
@@ -297,6 +311,11 @@ def run_long_context(steps: int, warmup: int, cpu_seconds: float = 0.0) -> dict:
         del graph
     if not torch.equal(outputs["pair"].view(torch.int16), outputs["fused"].view(torch.int16)):
         raise RuntimeError("fused append + attention differs from pc_kv_append + pc_paged_decode_attn")
+    if not torch.equal(pools["pair"].view(torch.int16), pools["fused"].view(torch.int16)):
+        raise RuntimeError("the fused call's pool differs from the pool pc_kv_append wrote")
+    _check_faults(workspace, "long_context_b256")
+    del pools["pair"]
+    pool = pools["fused"]
     total_ms = timings["fused"]
     attn = attention_bytes(w.lengths)
     append = w.batch * 1024 * 2  # read the new K/V rows, write them to their slots
@@ -627,6 +646,7 @@ def run_decode_step(steps: int, warmup: int) -> dict:
     attention_and_append()
     part = _captured(attention_and_append, device)
     part_ms = _timed(part.replay, steps, device)
+    _check_faults(graph._workspace, "decode_step_b128")  # the fault word is sticky: covers every step above
     kv_bytes = context * 1024 * LAYERS
     weight_bytes = sum(t.numel() * 2 for layer in weights.layers for t in (dec._fused(layer).qkv, layer.o_proj, dec._fused(layer).gate_up, layer.down_proj))
     weight_bytes += weights.lm_head.numel() * 2

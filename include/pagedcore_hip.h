@@ -86,13 +86,25 @@ int pc_kv_append(void* pool, int64_t num_blocks, int32_t layer_begin, int32_t nu
  * sequences). A sequence cut over several bins of one group leaves one fp32 partial per
  * part (all but its last) and kv head in `workspace`, with a ready flag; the bin holding
  * its last part waits for the flags (a bounded wait), folds the parts in order and writes
- * the row, then sets the flags back to zero. `workspace`: pc_attn_workspace_bytes() bytes,
+ * the row, then sets the flags back to zero. A flag value names the plan's epoch (each
+ * pc_attn_plan result has its own) and the layer, so a flag left raised by an earlier call
+ * is never taken for this call's partial. `workspace`: pc_attn_workspace_bytes() bytes,
  * 256-byte aligned, required (never null), ALL ZERO before its first use (hipMemset, or a
  * fill kernel under graph capture); every call leaves its flags at zero again, so it is
- * reused as is. Calls that share a workspace must not overlap in time. A part found
- * flagged by another XCD, or not flagged within the bounded wait, turns its sequence's rows
- * into NaN instead of reading a partial that may not be visible.
+ * reused as is. Calls that share a workspace must not overlap in time.
+ *
+ * Faults fail closed. The first 4 bytes of the workspace are its fault word (int32). A
+ * merge that finds a part flagged by another XCD (its partial may not be visible), or not
+ * flagged within the bounded wait, and a block id outside the pool turn the affected rows
+ * into NaN and OR a PC_ATTN_FAULT_* bit into the fault word; the call itself still returns
+ * PC_OK (the failure happens on the device, after the launch). The kernels never clear the
+ * word: the caller reads it after synchronizing and, when it is nonzero, treats every output
+ * since it was last cleared as failed and zeroes the whole workspace before reusing it.
  */
+#define PC_ATTN_WORKSPACE_HEADER_BYTES 256
+#define PC_ATTN_FAULT_MERGE_TIMEOUT 1 /* a part's flag was not raised within the bounded wait */
+#define PC_ATTN_FAULT_FOREIGN_XCD 2   /* a part's flag was raised on another XCD */
+#define PC_ATTN_FAULT_BLOCK_ID 4      /* a block id outside [0, num_blocks) */
 int pc_paged_decode_attn(void* out, const void* query, const void* pool, int64_t num_blocks, int32_t layer,
                          const int32_t* context_lens, int32_t batch, int32_t max_blocks, const int32_t* plan,
                          int32_t num_records, void* workspace, void* stream);
@@ -138,7 +150,8 @@ int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks);
  * frees nothing. Shapes whose workspace (pc_attn_workspace_bytes) exceeds the array are
  * refused with PC_ERR_ARGUMENT before any HIP call (32 MiB covers, e.g., batch 4096 with
  * 128-block tables, but not batch 8192). The array starts at zero when the library loads
- * and every call leaves its flags at zero. `stream` must belong to the current device.
+ * and every call leaves its flags at zero. Its fault word is not readable by the caller:
+ * a fault shows only as NaN rows. `stream` must belong to the current device.
  * Every call on one GPU
  * shares that GPU's array: calls that overlap in time on one GPU (concurrent streams,
  * threads) race and give wrong rows; calls ordered on one stream are safe. Arguments and
@@ -157,7 +170,7 @@ int pc_paged_decode_attn_noalloc(void* out, const void* query, const void* pool,
  * loaded of 8 groups (one per XCD); each group's blocks, taken sequence after sequence, are
  * cut into bins of equal block counts (about total / 256 blocks each, at least 8, at most
  * 256, and a bin also closes at 4 sequences). Row r holds bin r / 8 of group r % 8:
- *   {segments, blocks, 0 x 6},
+ *   {segments, blocks, plan epoch (nonzero, 22 bits, new for every call), 0 x 5},
  *   4 segments {sequence, context length, first block, blocks, row of the sequence's first
  *               bin, part index, parts, first partial slot (cut sequences) or 0},
  *   the bin's block ids in order (up to 256; 0 past them).

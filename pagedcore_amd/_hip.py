@@ -17,7 +17,7 @@ import numpy as np
 import torch
 from torch import Tensor
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 LIBRARY_NAME = "libpagedcore_hip.so"
 
 _lock = threading.Lock()
@@ -30,6 +30,52 @@ _i64 = ctypes.c_int64
 
 class HipExtensionError(RuntimeError):
     """The HIP library is missing, failed to load, or rejected a call."""
+
+
+# Attention workspace header (include/pagedcore_hip.h): the fault word, an int32 at byte 0
+# that the kernel ORs these bits into and never clears.
+WORKSPACE_HEADER_BYTES = 256
+FAULT_MERGE_TIMEOUT = 1
+FAULT_FOREIGN_XCD = 2
+FAULT_BLOCK_ID = 4
+_FAULT_TEXT = (
+    (FAULT_MERGE_TIMEOUT, "a cut sequence's part was not flagged within the bounded wait"),
+    (FAULT_FOREIGN_XCD, "a cut sequence's part was flagged on another XCD"),
+    (FAULT_BLOCK_ID, "a block id outside the pool"),
+)
+
+
+class AttentionFaultError(HipExtensionError):
+    """Paged attention failed on the device: the fault word of its workspace is nonzero.
+
+    The rows it names are NaN, and every output computed on that workspace since the word
+    was last cleared counts as failed. The workspace has been zeroed (flags and fault word)
+    when this is raised, so it can be used again; continuing to serve is the caller's
+    decision (DecodeWorker stops)."""
+
+    def __init__(self, faults: int, where: str) -> None:
+        text = "; ".join(name for bit, name in _FAULT_TEXT if faults & bit) or "unknown fault"
+        super().__init__(f"{where}: paged attention failed on the device (fault word {faults:#x}: {text})")
+        self.faults = faults
+
+
+def fault_word(workspace: Tensor) -> Tensor:
+    """The attention workspace's fault word as an int32 [1] view (device memory)."""
+    return workspace[:4].view(torch.int32)
+
+
+def raise_for_faults(faults: int, workspace: Tensor, where: str) -> None:
+    """Fail closed on a nonzero fault word read from `workspace`: zero the workspace (a fill
+    kernel on the current stream, never under graph capture) and raise AttentionFaultError."""
+    if faults:
+        workspace.zero_()
+        raise AttentionFaultError(int(faults), where)
+
+
+def check_attention_faults(workspace: Tensor, where: str) -> None:
+    """Read the workspace's fault word (synchronizing with the current stream) and fail
+    closed if it is nonzero."""
+    raise_for_faults(int(fault_word(workspace).item()), workspace, where)
 
 
 def library_path() -> str:
@@ -163,8 +209,9 @@ def _stream_key(device: torch.device) -> Tuple[int, int]:
 def attention_workspace(device: torch.device, nbytes: int) -> Tensor:
     """Split-K partial scratch for the current stream of `device`, grown on demand.
 
-    Zero-initialized: the part flags in it must start at zero, and every call leaves them
-    so. Reuse is safe because every call that uses it is ordered on that one stream.
+    Zero-initialized: the part flags and the fault word in it must start at zero, and every
+    call leaves the flags so (a fault is cleared by raise_for_faults). Reuse is safe because
+    every call that uses it is ordered on that one stream.
     """
     key = _stream_key(device)
     workspace = _workspaces.get(key)
@@ -239,14 +286,16 @@ def paged_decode_attention(
     *,
     plan: Optional[Tensor] = None,
     workspace: Optional[Tensor] = None,
-) -> None:
+) -> Tensor:
     """out[b] = paged decode attention of query[b] over layer `layer` of the pool.
 
     out/query: fp16 [batch, 32, 64] contiguous; block_tables: int32 [batch, max_blocks];
     context_lens: int32 [batch] contiguous. All on the pool's device. `plan`: the
     decode_plan() rows for the same lengths and tables as a contiguous int32 device tensor
     (None: built here from host copies, which synchronizes). `workspace` (uint8, zero before
-    its first use; every call leaves it so) defaults to the per-stream cached buffer.
+    its first use; every call leaves its flags so) defaults to the per-stream cached buffer.
+    Returns the workspace used, whose fault word (fault_word) the caller checks once it
+    synchronizes.
     """
     lib = load()
     batch, max_blocks = block_tables.shape
@@ -258,6 +307,7 @@ def paged_decode_attention(
     if plan is None:
         plan = torch.from_numpy(decode_plan(context_lens.cpu().numpy(), block_tables.cpu().numpy())).to(pool.device)
     planned_decode_attention(out, query, pool, layer, context_lens, plan, max_blocks, workspace)
+    return workspace
 
 
 def planned_decode_attention(
@@ -267,7 +317,8 @@ def planned_decode_attention(
     """pc_paged_decode_attn with a ready device plan (decode_plan() rows, possibly padded
     with empty rows) for a batch of context_lens.shape[0] rows whose tables are at most
     max_blocks wide; workspace of workspace_bytes(batch, max_blocks) bytes, zero before its
-    first use (every call leaves it so).
+    first use (every call leaves its flags so; a device fault sets its fault word, which
+    the caller checks: check_attention_faults).
 
     With new_key and new_value (fp16 [batch, 4, 64] contiguous, the token at position
     context_lens[b] - 1 of each sequence) the call is pc_kv_append_paged_decode_attn: the

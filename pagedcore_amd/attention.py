@@ -8,6 +8,11 @@ one final fp16 rounding, autocast ignored. The two page traversals of the refere
 replaced by one launch of the HIP paged-attention kernels, which walk the block table on
 the device; nothing larger than the output is materialised from the pool.
 
+Both entry points fail closed on a device-side failure of the launch (a cut sequence's
+merge that timed out or saw another XCD's flag, a block id outside the pool): they read
+the workspace's fault word after the launch, which synchronizes, and raise
+AttentionFaultError (a RuntimeError) instead of returning NaN rows.
+
 ``paged_attention_batch`` is the batched form the decode loop needs (one launch for all
 rows of a layer). The reference's ``eager_rounding=True`` path replays HF fp16 rounding for
 forensic comparisons; it is not part of the serving path and is rejected here.
@@ -15,7 +20,7 @@ forensic comparisons; it is not part of the serving path and is rejected here.
 
 from __future__ import annotations
 
-from typing import Optional, Sequence
+from typing import Sequence, Tuple
 
 import torch
 from torch import Tensor
@@ -33,12 +38,15 @@ def _check_layer(layer_index: int) -> None:
         raise ValueError("layer_index must identify one of the 22 decoder layers")
 
 
-def _launch(
+def attend_rows(
     query: Tensor,
     allocator: KVAllocator,
     request_ids: Sequence[RequestId],
     layer_index: int,
-) -> Tensor:
+) -> Tuple[Tensor, Tensor]:
+    """One launch of paged attention for already validated rows; returns the output and
+    the workspace whose fault word the caller must check (check_attention_faults) before
+    it trusts the output. Nothing synchronizes."""
     tables, lengths = allocator.gather_block_tables(request_ids, layer_index=layer_index)
     pool = allocator.pool
     if pool.device != query.device:
@@ -51,7 +59,13 @@ def _launch(
         q = q.contiguous()
     out = torch.empty((batch, Q_HEADS, 1, HEAD_DIM), dtype=torch.float16, device=query.device)
     plan = allocator.decode_plan(request_ids, layer_index=layer_index)
-    _hip.paged_decode_attention(out, q, pool, layer_index, tables, lengths, plan=plan)
+    workspace = _hip.paged_decode_attention(out, q, pool, layer_index, tables, lengths, plan=plan)
+    return out, workspace
+
+
+def _checked(query, allocator, request_ids, layer_index, where) -> Tensor:
+    out, workspace = attend_rows(query, allocator, request_ids, layer_index)
+    _hip.check_attention_faults(workspace, where)
     return out
 
 
@@ -70,7 +84,7 @@ def paged_attention(
     _check_layer(layer_index)
     if eager_rounding:
         raise ValueError("eager_rounding replays HF fp16 rounding and is not part of the GPU path")
-    return _launch(query, allocator, (request_id,), layer_index)
+    return _checked(query, allocator, (request_id,), layer_index, "paged_attention")
 
 
 @torch.inference_mode()
@@ -88,4 +102,4 @@ def paged_attention_batch(
     if len(set(request_ids)) != batch:
         raise ValueError("attention requires distinct request IDs")
     _check_layer(layer_index)
-    return _launch(query, allocator, tuple(request_ids), layer_index)
+    return _checked(query, allocator, tuple(request_ids), layer_index, "paged_attention_batch")

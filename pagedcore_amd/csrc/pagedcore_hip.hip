@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -64,7 +65,7 @@ using pc_internal::check_launch;
 using pc_internal::ok;
 using pc_internal::set_error;
 
-constexpr int kAbiVersion = 12;
+constexpr int kAbiVersion = 13;
 constexpr int kLayers = 22;
 constexpr int kSlots = 16;
 constexpr int kKVHeads = 4;
@@ -212,8 +213,10 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_word_kernel(
 // cannot deadlock) stages each part in LDS as its flag rises, combines them in span order
 // with its own last (their max first, then the weighted sums), writes the output and lowers
 // the flags. Partials and flags stay in the XCD's L2 (plain
-// stores and loads are coherent there); the flag carries the writer's XCD id and a merge
-// that sees another XCD's id writes NaN rows instead of reading stale partials.
+// stores and loads are coherent there); the flag carries the plan's epoch, the layer and
+// the writer's XCD id: a flag of another epoch or layer is not this call's and is waited
+// past, and a merge that sees this call's flag with another XCD's id writes NaN rows
+// instead of reading stale partials and records the fault in the workspace.
 // ---------------------------------------------------------------------------------------
 
 constexpr int kBinThreads = 64 * kKVHeads;         // one wave per kv head
@@ -222,7 +225,7 @@ constexpr int kMaxSegs = 4;                        // sequences per bin
 constexpr int kMaxUnits = 256;                     // blocks per bin
 constexpr int kUnitBytes = 4096;                   // K (2 KiB) then V (2 KiB) of one head of one block
 constexpr int kWaveLds = kRing * kUnitBytes + 2 * kMaxSegs * 1024;  // ring, Q and output per segment
-constexpr int kHeaderInts = 8;                     // {segments, blocks, 0 x 6}
+constexpr int kHeaderInts = 8;                     // {segments, blocks, plan epoch, 0 x 5}
 constexpr int kSegInts = 8;                        // {sequence, length, first block, blocks, first bin, part, parts, first slot}
 constexpr int kRecordInts = kHeaderInts + kMaxSegs * kSegInts;
 constexpr int kRowInts = kRecordInts + kMaxUnits;  // one plan row: the record, then the block ids
@@ -232,6 +235,19 @@ constexpr int kMinBinBlocks = 8;                   // smaller workloads use fewe
 constexpr int kSlotBytes = 2176;                   // partial: O (2 KiB, lane-major), (m, l) x 8, flag; 17 lines
 constexpr int kFlagOffset = 2112;
 constexpr int kMaxSpins = 100000;                  // bounded wait for a part's flag
+constexpr int kWorkspaceHeader = PC_ATTN_WORKSPACE_HEADER_BYTES;  // the fault word, then reserved
+constexpr uint32_t kEpochMask = (1u << 22) - 1;    // plan epochs occupy flag bits 9..30
+static_assert(kWorkspaceHeader % 256 == 0, "partial slots keep the workspace's 256-byte alignment");
+
+// A raised part flag: the plan's epoch in bits 9..30, the layer in bits 4..8 and the
+// writer's XCD id + 1 in bits 0..3. A flag counts for a call only if its epoch and layer
+// are the call's, so a flag left raised by an earlier call (a producer whose merge gave up
+// waiting, or a plan without a merging row) is never taken for this call's partial: the
+// merge keeps waiting until this call's producer overwrites it.
+__device__ __forceinline__ int flag_key(int epoch, int layer) {
+  return static_cast<int>(((static_cast<uint32_t>(epoch) & kEpochMask) << 9) | (static_cast<uint32_t>(layer) << 4));
+}
+__device__ __forceinline__ bool flag_of_call(int f, int key) { return (f & 0xF) != 0 && (f & ~0xF) == key; }
 // Scale of the low (remainder) part of p in the PV product (2^18).
 constexpr float kLowScale = 262144.0f;
 // Headroom (log2 of p) before the running max is raised.
@@ -415,7 +431,8 @@ __device__ __forceinline__ Part combine_staged(const char* stage, int n, int lan
 }
 
 // Workspace slot of part k of a cut sequence whose parts start at slot `first` (the plan
-// numbers the parts of all cut sequences densely; the last part has no slot).
+// numbers the parts of all cut sequences densely; the last part has no slot). `slots` is
+// the workspace past its header.
 __device__ __forceinline__ char* part_slot(char* slots, int first, int k, int h) {
   return slots + ((static_cast<int64_t>(first) + k) * kKVHeads + h) * kSlotBytes;
 }
@@ -428,17 +445,23 @@ __device__ __forceinline__ char* part_slot(char* slots, int first, int k, int h)
 // holding the sequence's last block stages the row in LDS with the Q DMAs, and once that
 // block's DMA has landed copies the row into its ring slot (so this pass already reads it)
 // and stores it to the pool.
+//
+// Faults. A merge that gives up waiting (PC_ATTN_FAULT_MERGE_TIMEOUT), a part flag raised
+// on another XCD (PC_ATTN_FAULT_FOREIGN_XCD) and a block id outside the pool
+// (PC_ATTN_FAULT_BLOCK_ID) turn the affected rows into NaN and are ORed into the
+// workspace's fault word by one lane's vector atomic. The kernel never clears the word.
 template <bool APPEND>
 __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int32_t* plan, const _Float16* query,
                                                                       _Float16* pool, int64_t num_blocks,
                                                                       int layer, int batch, int nslots, _Float16* out,
-                                                                      char* slots, const _Float16* new_key,
+                                                                      char* workspace, const _Float16* new_key,
                                                                       const _Float16* new_value) {
   __shared__ __attribute__((aligned(16))) char lds[kKVHeads * kWaveLds];
   const int h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, g = lane >> 4;
   const int32_t* row = plan + static_cast<int64_t>(blockIdx.x) * kRowInts;
+  char* const slots = workspace + kWorkspaceHeader;
 
   // The record (scalar loads) and the bin's block ids (lane L of vector k holds id 64 k + L)
   // in one round trip: the id addresses do not depend on the record.
@@ -451,6 +474,10 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : "+v"(idv[0]), "+v"(idv[1]), "+v"(idv[2]), "+v"(idv[3]) :: "memory");
   const int nseg = rec[0], nunits = rec[1];
   if (nseg <= 0 || nseg > kMaxSegs || nunits <= 0 || nunits > kMaxUnits) return;  // padding rows do nothing
+  // This call's flag values (the plan's epoch and the layer; the XCD id is added where a flag
+  // is raised), held in a VGPR: the stream loop needs every SGPR it has.
+  int key;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(key) : "s"(flag_key(rec[2], layer)));
 
   char* wl = lds + h * kWaveLds;
   char* ring = wl;
@@ -699,13 +726,13 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
   auto slots_ok = [&](int first, int parts) { return first >= 0 && parts >= 2 && first + static_cast<int64_t>(parts) - 1 <= nslots; };
 
   // A part that is not the last of its span: store it, wait for the acknowledgement, then
-  // raise the part's flag (the writer's XCD id + 1 in bits 8..15, 1 in bits 0..7).
+  // raise the part's flag.
   if (complete && nspanl > 1 && kidxl < nspanl - 1 && kidxl >= 0 && slots_ok(slotl, nspanl)) {
     char* slot = part_slot(slots, slotl, kidxl, h);
     store_part(slot, lane, last_part);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (lane == 0) {
-      __hip_atomic_store(reinterpret_cast<int32_t*>(slot + kFlagOffset), 1 + ((xcc_id() + 1) << 8), __ATOMIC_RELAXED,
+      __hip_atomic_store(reinterpret_cast<int32_t*>(slot + kFlagOffset), key | (xcc_id() + 1), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -724,11 +751,18 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
   // order and this bin's part last, write the rows, lower the flags. This code stays small
   // and its loops rolled: it runs once per merge, cold in the instruction cache, where every
   // 64-byte line fetched costs an L2 round trip.
+  // A block id outside the pool anywhere in the bin (lane L of vector k holds id 64 k + L).
+  bool any_bad = false;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    any_bad |= __builtin_amdgcn_ballot_w64(64 * k + lane < nunits && static_cast<uint32_t>(idv[k]) >= num_blocks) != 0;
+  }
+  int fault = any_bad ? PC_ATTN_FAULT_BLOCK_ID : 0;
   if (complete && nspan0 > 1 && kidx0 == nspan0 - 1 && slots_ok(slot0, nspan0) &&
       k00 + static_cast<int64_t>(kGroups) * kidx0 == static_cast<int64_t>(blockIdx.x) && k00 >= 0) {
-    const int want = 1 + ((xcc_id() + 1) << 8);
+    const int want = key | (xcc_id() + 1);
     const int nparts = nspan0 - 1;  // parts 0 .. nspan0 - 2 are in the workspace
-    bool ok = true;
+    bool timeout = false, foreign = false;
     Part acc_p;
     if (nparts <= kStageParts) {
       // One chunk: lane k polls part k's flag (lanes past the span repeat the last part's),
@@ -741,12 +775,13 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
 #pragma nounroll
       while (pending != 0) {
         const int f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool raised = flag_of_call(f, key);
         // raised on another XCD: its partial is not visible here
-        if (__builtin_amdgcn_ballot_w64(lane < nparts && f != 0 && f != want) != 0) ok = false;
-        uint64_t ready = __builtin_amdgcn_ballot_w64(f != 0) & pending;
+        if (__builtin_amdgcn_ballot_w64(lane < nparts && raised && f != want) != 0) foreign = true;
+        uint64_t ready = __builtin_amdgcn_ballot_w64(raised) & pending;
         if (ready == 0) {
           if (++spins >= kMaxSpins) {  // never raised: the rows become NaN
-            ok = false;
+            timeout = true;
             break;
           }
           __builtin_amdgcn_s_sleep(2);
@@ -773,10 +808,11 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
 #pragma nounroll
         for (int spins = 0; spins < kMaxSpins; ++spins) {
           f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (__builtin_amdgcn_ballot_w64(f == 0) == 0) break;
+          if (__builtin_amdgcn_ballot_w64(!flag_of_call(f, key)) == 0) break;
           __builtin_amdgcn_s_sleep(2);
         }
-        if (__builtin_amdgcn_ballot_w64(f != want) != 0) ok = false;
+        if (__builtin_amdgcn_ballot_w64(!flag_of_call(f, key)) != 0) timeout = true;
+        if (__builtin_amdgcn_ballot_w64(flag_of_call(f, key) && f != want) != 0) foreign = true;
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -795,12 +831,13 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
       }
       fold_part(acc_p, first_part);
     }
-    if (!ok) {
+    if (timeout || foreign) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         acc_p.o[0][r] = NAN;
         acc_p.o[1][r] = NAN;
       }
+      fault |= (timeout ? PC_ATTN_FAULT_MERGE_TIMEOUT : 0) | (foreign ? PC_ATTN_FAULT_FOREIGN_XCD : 0);
     }
     if (b0 >= 0 && b0 < batch) {
       wave_lds_fence();
@@ -813,6 +850,10 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
       __hip_atomic_store(reinterpret_cast<int32_t*>(part_slot(slots, slot0, k, h) + kFlagOffset), 0, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
+  // `fault` is uniform over the wave; one lane ORs it into the fault word.
+  if (fault != 0 && lane == 0) {
+    __hip_atomic_fetch_or(reinterpret_cast<int32_t*>(workspace), fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -851,7 +892,8 @@ int64_t slots_bound(int32_t batch, int32_t max_blocks) {
   return kTargetBins + (total + kMaxUnits - 1) / kMaxUnits + 2 * kGroups + (batch + kMaxSegs - 2) / (kMaxSegs - 1);
 }
 
-int64_t workspace_bytes_for(int64_t slots) { return slots * kKVHeads * kSlotBytes; }
+// The header (fault word), then the partial slots.
+int64_t workspace_bytes_for(int64_t slots) { return kWorkspaceHeader + slots * kKVHeads * kSlotBytes; }
 
 // Split-K scratch of pc_paged_decode_attn_noalloc: a file-scope device array, one copy per
 // GPU, held until the process ends. Host code never passes `scratch` itself to a kernel (in
@@ -910,6 +952,19 @@ int launch_decode_attn(void* out, const void* query, void* pool, int64_t num_blo
                      static_cast<int>(nslots), static_cast<_Float16*>(out), static_cast<char*>(workspace),
                      static_cast<const _Float16*>(new_key), static_cast<const _Float16*>(new_value));
   return check_launch(APPEND ? "kv_append_paged_decode_bin" : "paged_decode_bin");
+}
+
+// Plan epochs: every plan gets the next nonzero 22-bit value, stamped into each of its rows
+// (header int 2). Part flags carry it, so a flag raised under another plan is never taken
+// for this plan's.
+std::atomic<uint32_t> g_plan_epoch{0};
+
+uint32_t next_plan_epoch() {
+  uint32_t e;
+  do {
+    e = (g_plan_epoch.fetch_add(1, std::memory_order_relaxed) + 1) & kEpochMask;
+  } while (e == 0);
+  return e;
 }
 
 // One bin while it is being cut: its segments {sequence, first block, blocks}.
@@ -1046,6 +1101,7 @@ int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, i
                       static_cast<long long>(slots), static_cast<long long>(slots_bound(batch, max_blocks)));
   }
   std::fill(plan, plan + rows * kRowInts, 0);
+  const int32_t epoch = static_cast<int32_t>(next_plan_epoch());
   for (int x = 0; x < kGroups; ++x) {
     for (size_t i = 0; i < bins[x].size(); ++i) {
       const BinSegs& bs = bins[x][i];
@@ -1053,6 +1109,7 @@ int32_t pc_attn_plan(const int32_t* context_lens, const int32_t* block_tables, i
       int32_t* row = plan + static_cast<int64_t>(r) * kRowInts;
       row[0] = bs.nseg;
       row[1] = bs.blocks;
+      row[2] = epoch;
       int u = 0;
       for (int s = 0; s < bs.nseg; ++s) {
         const int32_t b = bs.seg[s][0], j0 = bs.seg[s][1], n = bs.seg[s][2];

@@ -38,7 +38,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from pagedcore_amd import _hip
-from pagedcore_amd.attention import paged_attention_batch
+from pagedcore_amd.attention import attend_rows
 from pagedcore_amd.engine_types import RequestId
 from pagedcore_amd.kv_cache import CONTEXT_LIMIT, HEAD_DIM, KV_HEADS, LAYERS, KVAllocator
 
@@ -317,7 +317,10 @@ def decode_paged(
     request_ids[b], at position = its cached length); returns fp16 logits [B, 1, vocab].
 
     Each request gains one cached position on success; on any exception the staged step
-    is discarded and no request changes (reference src/pagedcore/decoder.py:156-199).
+    is discarded and no request changes (reference src/pagedcore/decoder.py:156-199). A
+    device-side attention failure counts as one: the step reads the attention workspaces'
+    fault words before it commits (one synchronization per step) and raises
+    AttentionFaultError instead of returning logits computed from NaN rows.
     """
     request_ids = tuple(request_ids)
     if input_ids.dtype != torch.int64 or input_ids.ndim != 2 or input_ids.shape != (len(request_ids), 1):
@@ -334,15 +337,20 @@ def decode_paged(
         x = torch.empty_like(hidden)
         _hip.add_rms_norm(x, hidden, None, weights.layers[0].input_norm, RMS_EPS)
         batch = len(request_ids)
+        workspaces: Dict[int, Tensor] = {}
         for index, layer in enumerate(weights.layers):
 
             def attend(qkv: Tensor, index: int = index) -> Tensor:
                 query = allocator.write_decode_layers_rotary(request_ids, index, qkv, table)
-                return paged_attention_batch(query, allocator, request_ids, layer_index=index).view(batch, HIDDEN)
+                out, workspace = attend_rows(query, allocator, request_ids, index)
+                workspaces[workspace.data_ptr()] = workspace
+                return out.view(batch, HIDDEN)
 
             following = weights.layers[index + 1].input_norm if index + 1 < LAYERS else weights.final_norm
             _attention_block(x, hidden, layer, _fused(layer), following, attend)
         logits = F.linear(x, weights.lm_head)
+        for workspace in workspaces.values():
+            _hip.check_attention_faults(workspace, "decode_paged")
     return logits.unsqueeze(1)
 
 
@@ -366,6 +374,12 @@ class DecodeGraph:
     the plan into a pinned buffer, uploads the rows in use (and the empty rows that replace
     a longer previous plan) with two asynchronous copies and replays the graph; nothing
     synchronizes.
+
+    Device faults fail closed. After each replay the attention workspace's fault word is
+    copied to pinned memory. check_faults() raises AttentionFaultError if the last step's
+    attention failed on the device (call it after reading the step's logits, as
+    DecodeWorker does), and every step first waits for the step two before it and raises
+    if that step failed, before staging anything. On a raise the workspace is zeroed.
 
     Same checks, errors and staged-append semantics as decode_paged for any 1 to `batch`
     requests (any requests, in any order, step to step). A batch of exactly `batch`
@@ -400,8 +414,9 @@ class DecodeGraph:
         self._plan = self._inputs32[self._lens_span :].view(self._capacity, fields)
         self._fields = fields
         self._workspace = torch.zeros(max(256, _hip.workspace_bytes(batch, MAX_BLOCKS)), dtype=torch.uint8, device=device)
-        # Two pinned staging buffers used in turn; an event marks when a buffer's upload
-        # has run, so it is not refilled while its copy may still be pending.
+        # Two pinned staging buffers used in turn, each with a pinned copy of the fault word
+        # after its step; an event marks when that step has finished, so a buffer is not
+        # refilled while its upload may still be pending and its fault copy is complete.
         self._host = [
             (
                 torch.empty((3, batch), dtype=torch.int64, pin_memory=True),
@@ -409,7 +424,9 @@ class DecodeGraph:
             )
             for _ in range(2)
         ]
-        self._uploaded: list = [None, None]
+        self._fault_host = [torch.zeros(1, dtype=torch.int32, pin_memory=True) for _ in range(2)]
+        self._finished: list = [None, None]
+        self._last_turn: Optional[int] = None
         self._host_rows = [0, 0]  # plan rows a pinned buffer may hold non-empty
         self._device_rows = 0  # plan rows the device buffer may hold non-empty
         self._turn = 0
@@ -450,10 +467,27 @@ class DecodeGraph:
             _attention_block(x, hidden, layer, _fused(layer), following, attend)
         return F.linear(x, weights.lm_head)
 
+    def _take_faults(self, turn: int) -> None:
+        """Wait for the step that last used staging buffer `turn` and fail closed if its copy
+        of the workspace's fault word is nonzero (each copy is checked once)."""
+        finished = self._finished[turn]
+        if finished is None:
+            return
+        finished.synchronize()
+        self._finished[turn] = None
+        _hip.raise_for_faults(int(self._fault_host[turn][0]), self._workspace, "DecodeGraph.step")
+
+    def check_faults(self) -> None:
+        """Raise AttentionFaultError if the last step's attention failed on the device. Waits
+        for that step (a caller that already read its logits has waited for it)."""
+        if self._last_turn is not None:
+            self._take_faults(self._last_turn)
+
     @torch.inference_mode()
     def step(self, input_ids: Tensor, request_ids: Tuple[RequestId, ...]) -> Tensor:
         """decode_paged(input_ids, weights, allocator, request_ids) by graph replay, for 1 to
-        `batch` requests. Returns fresh fp16 logits [len(request_ids), 1, vocab]."""
+        `batch` requests. Returns fresh fp16 logits [len(request_ids), 1, vocab]; the caller
+        checks them with check_faults() once it has synchronized."""
         request_ids = tuple(request_ids)
         if input_ids.dtype != torch.int64 or input_ids.ndim != 2 or input_ids.shape != (len(request_ids), 1):
             raise ValueError("input_ids must be int64 [batch, 1] matching request IDs")
@@ -468,9 +502,8 @@ class DecodeGraph:
         with allocator.append_decode(request_ids):
             staged = allocator.staged_decode(request_ids, width=MAX_BLOCKS)
             turn = self._turn
+            self._take_faults(turn)
             self._turn ^= 1
-            if self._uploaded[turn] is not None:
-                self._uploaded[turn].synchronize()
             host64, host32 = self._host[turn]
             h64 = host64.numpy()
             h32 = host32.numpy()
@@ -488,11 +521,13 @@ class DecodeGraph:
             self._device_rows = count
             self._inputs64[1:].copy_(host64[1:], non_blocking=True)
             self._inputs32[:upload].copy_(host32[:upload], non_blocking=True)
-            uploaded = torch.cuda.Event()
-            uploaded.record()
-            self._uploaded[turn] = uploaded
             self._inputs64[0, :rows].copy_(input_ids[:, 0])
             self._graph.replay()
+            self._fault_host[turn].copy_(_hip.fault_word(self._workspace), non_blocking=True)
+            finished = torch.cuda.Event()
+            finished.record()
+            self._finished[turn] = finished
+            self._last_turn = turn
             allocator.record_decode_writes(request_ids, LAYERS)
             logits = self._logits[:rows].clone()
         return logits.unsqueeze(1)

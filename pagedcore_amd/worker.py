@@ -20,6 +20,12 @@ iteration"); its single-request greedy semantics are src/pagedcore/decoder.py:61
 Everything runs on the allocator's worker thread and stream, so a release is ordered after
 every launch that read the released blocks (the reference's stream-ordered reuse rule,
 docs/DESIGN.md:282).
+
+A device-side failure fails closed (the reference's rule for unsafe device failures,
+docs/DESIGN.md:178,255,282): when a decode step's paged attention reports a fault (its
+workspace's fault word, read right after the step's tokens are fetched and before any is
+emitted), the iteration raises AttentionFaultError and the worker stops: every later step()
+raises RuntimeError, and nothing more is launched.
 """
 
 from __future__ import annotations
@@ -32,6 +38,7 @@ from typing import Callable, Deque, Dict, List, Optional, Sequence, Tuple, Union
 import torch
 from torch import Tensor
 
+from pagedcore_amd._hip import AttentionFaultError
 from pagedcore_amd.engine_types import KVReservation, RequestId
 from pagedcore_amd.kv_cache import BLOCK_TOKENS, CONTEXT_LIMIT, KVAllocator
 
@@ -155,6 +162,7 @@ class DecodeWorker:
         self._cancelled: set = set()
         self._results: Dict[RequestId, GreedyResult] = {}
         self._known: set = set()
+        self._fault: Optional[AttentionFaultError] = None
 
     # -- queue -----------------------------------------------------------------------------
 
@@ -194,8 +202,22 @@ class DecodeWorker:
 
     # -- one iteration -----------------------------------------------------------------------
 
+    @property
+    def fault(self) -> Optional[AttentionFaultError]:
+        """The device fault that stopped the worker, or None."""
+        return self._fault
+
     def step(self) -> List[Tuple[RequestId, int]]:
         """Run one scheduler iteration; returns the (request, token) pairs emitted."""
+        if self._fault is not None:
+            raise RuntimeError("the decode worker stopped after a device fault") from self._fault
+        try:
+            return self._iterate()
+        except AttentionFaultError as error:
+            self._fault = error
+            raise
+
+    def _iterate(self) -> List[Tuple[RequestId, int]]:
         self._cleanup()
         emitted: List[Tuple[RequestId, int]] = []
         self._admit_one(emitted)
@@ -204,8 +226,10 @@ class DecodeWorker:
             tokens = torch.tensor(
                 [[self._active[rid].selected[-1]] for rid in batch], dtype=torch.int64, device=self._device()
             )
-            logits = self._decode_batch(tokens, batch)
+            logits, graph = self._decode_batch(tokens, batch)
             chosen = logits[:, -1].argmax(dim=-1).tolist()
+            if graph is not None:
+                graph.check_faults()  # decode_paged checks inside its step
             for rid, token in zip(batch, chosen):
                 self._select(rid, int(token), emitted)
         return emitted
@@ -286,11 +310,13 @@ class DecodeWorker:
         for size in self._prompt_sizes:
             self._prefill_graph_for(size)
 
-    def _decode_batch(self, tokens: Tensor, batch: Tuple[RequestId, ...]) -> Tensor:
+    def _decode_batch(self, tokens: Tensor, batch: Tuple[RequestId, ...]):
+        """The step's logits, and the DecodeGraph that ran it (None for eager decoding)."""
         size = next((size for size in self._graph_sizes if size >= len(batch)), None)
         if size is not None:
-            return self._graph_for(size).step(tokens, batch)
-        return self._decode(tokens, self._weights, self._allocator, batch)
+            graph = self._graph_for(size)
+            return graph.step(tokens, batch), graph
+        return self._decode(tokens, self._weights, self._allocator, batch), None
 
     def _select(self, rid: RequestId, token: int, emitted: List[Tuple[RequestId, int]]) -> None:
         state = self._active[rid]

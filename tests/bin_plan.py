@@ -2,11 +2,13 @@
 restating what the attention kernel reads from each plan row and which workspace slots it
 touches, so that every index the kernel derives from a plan is shown in range on the CPU.
 
-Plan row (pc_attn_plan_record_ints() int32): {segments, blocks, 0 x 6}, then 4 segments of
+Plan row (pc_attn_plan_record_ints() int32): {segments, blocks, plan epoch, 0 x 5}, then 4 segments of
 {sequence, length, first block, blocks, first bin, part, parts, first slot}, then the
 bin's block ids (up to 256). Row r belongs to group r % 8; the bins of a cut sequence are
 rows first bin + 8 k of one group; parts 0 .. parts - 2 have workspace slots
-first slot + k (the last part is folded in registers).
+first slot + k (the last part is folded in registers). Every live row of one plan carries the
+same nonzero 22-bit epoch. The workspace is a 256-byte header (the fault word), then the
+partial slots.
 """
 
 from __future__ import annotations
@@ -24,6 +26,8 @@ ROW = RECORD + MAX_UNITS
 GROUPS = 8
 HEADS = 4
 SLOT_BYTES = 2176
+WORKSPACE_HEADER = 256
+EPOCH_LIMIT = 1 << 22
 
 
 def check_decode_plan(plan: np.ndarray, lengths: np.ndarray, tables: np.ndarray, num_blocks: int,
@@ -38,8 +42,9 @@ def check_decode_plan(plan: np.ndarray, lengths: np.ndarray, tables: np.ndarray,
     batch = len(lengths)
     nblk = [(int(x) + 15) // 16 if x > 0 else 0 for x in lengths]
     parts: Dict[int, List[tuple]] = {}
-    slots_needed = workspace_bytes // (HEADS * SLOT_BYTES)
+    slots_needed = (workspace_bytes - WORKSPACE_HEADER) // (HEADS * SLOT_BYTES)
     used_slots = set()
+    epochs = set()
     live = most = 0
     for r in range(rows):
         row = plan[r]
@@ -48,7 +53,9 @@ def check_decode_plan(plan: np.ndarray, lengths: np.ndarray, tables: np.ndarray,
             assert not row.any(), f"padding row {r} is not empty"
             continue
         live += 1
-        assert 1 <= nseg <= MAX_SEGS and 1 <= nunits <= MAX_UNITS and not row[2:HEADER].any()
+        assert 1 <= nseg <= MAX_SEGS and 1 <= nunits <= MAX_UNITS and not row[3:HEADER].any()
+        assert 0 < int(row[2]) < EPOCH_LIMIT
+        epochs.add(int(row[2]))
         most = max(most, nunits)
         u = 0
         for s in range(nseg):
@@ -71,6 +78,7 @@ def check_decode_plan(plan: np.ndarray, lengths: np.ndarray, tables: np.ndarray,
         assert u == nunits and not row[RECORD + nunits:].any()
         for s in range(nseg, MAX_SEGS):
             assert not row[HEADER + SEG * s: HEADER + SEG * (s + 1)].any()
+    assert len(epochs) <= 1, "live rows of one plan carry different epochs"
     cut = 0
     for b in range(batch):
         got = sorted(parts.get(b, []))

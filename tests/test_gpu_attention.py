@@ -22,35 +22,16 @@ from oracle import paged_reference as ref
 from pagedcore_amd import _hip
 from tests import workloads
 from tests.bin_plan import check_decode_plan, regrouped_plan
+from tests.support import ATOL, assert_max_abs, fault_word, flags_clear, workspace_flags
 from pagedcore_amd.attention import paged_attention, paged_attention_batch
 from pagedcore_amd.engine_types import CapacityCounts, KVReservation, RequestId
 from pagedcore_amd.kv_cache import KVAllocator
 
 pytestmark = pytest.mark.gpu
 
-ATOL = 2e-3  # max-abs bound on fp16 attention outputs; no relative term
-
-
 def _say(*parts) -> None:
     print(*parts, flush=True)
     sys.stdout.flush()
-
-
-def assert_max_abs(got, expected, what: str = "", atol: float = ATOL, rtol: float = 0.0) -> float:
-    """max |got - expected| <= atol (elementwise, in float64); both must be finite. Returns
-    the error. rtol > 0 is only for the reference's own cases with a bound tighter than
-    2e-3 (atol + rtol * |expected| there, as its assert_close), and the 2e-3 max-abs bound
-    holds as well."""
-    got64 = got.detach().cpu().double()
-    expected64 = expected.detach().cpu().double().reshape(got64.shape)
-    assert torch.isfinite(got64).all(), f"{what}: non-finite output"
-    assert torch.isfinite(expected64).all(), f"{what}: non-finite expectation"
-    difference = (got64 - expected64).abs()
-    error = difference.max().item() if got64.numel() else 0.0
-    assert error <= ATOL, f"{what}: max |got - expected| = {error:.3e} > {ATOL:.1e}"
-    excess = (difference - (atol + rtol * expected64.abs())).max().item() if got64.numel() else 0.0
-    assert excess <= 0, f"{what}: max |got - expected| = {error:.3e} exceeds atol {atol:.1e} + rtol {rtol:.1e} * |expected|"
-    return error
 
 
 class Worst:
@@ -548,22 +529,95 @@ def test_block_table_indirection_is_invisible(device):
 
 def test_out_of_range_block_id_poisons_only_its_row(device):
     """A table entry outside the pool never reads out of bounds: that row's output is NaN,
-    the other rows are unaffected."""
+    the other rows are unaffected, and the fault is recorded in the workspace's fault word:
+    the fault check raises AttentionFaultError and clears the workspace."""
     w = workloads.batched_decode(batch=4, num_blocks=512, lo=40, hi=300, seed=47)
     pool = _random_pool(device, w.num_blocks, 15)
     queries = torch.from_numpy(w.queries(0)).to(device)
     tables = torch.from_numpy(w.tables).to(device)
     lens = torch.from_numpy(w.lengths).to(device)
     good = torch.empty_like(queries)
-    _hip.paged_decode_attention(good, queries, pool, 0, tables, lens)
+    workspace = _hip.paged_decode_attention(good, queries, pool, 0, tables, lens)
+    assert fault_word(workspace) == 0
     broken = tables.clone()
     broken[2, 1] = w.num_blocks + 7
     bad = torch.empty_like(queries)
-    _hip.paged_decode_attention(bad, queries, pool, 0, broken, lens)
+    assert _hip.paged_decode_attention(bad, queries, pool, 0, broken, lens) is workspace
     torch.cuda.synchronize()
     assert torch.isnan(bad[2]).all()
     for b in (0, 1, 3):
         assert torch.equal(bad[b], good[b])
+    assert fault_word(workspace) == _hip.FAULT_BLOCK_ID
+    with pytest.raises(_hip.AttentionFaultError, match="outside the pool"):
+        _hip.check_attention_faults(workspace, "test")
+    assert fault_word(workspace) == 0 and flags_clear(workspace)
+
+
+def _one_token_cache(device):
+    pool = torch.full((22, 2, 4, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
+    allocator = KVAllocator(pool)
+    request = RequestId("one")
+    allocator.create(KVReservation(request, 1))
+    key = torch.zeros(22, 1, 4, 64, dtype=torch.float16, device=device)
+    allocator.append(request, key, key)
+    return allocator, request
+
+
+@pytest.mark.parametrize(
+    "shape,dtype",
+    [((2, 32, 1, 64), torch.float16), ((1, 31, 1, 64), torch.float16), ((1, 32, 2, 64), torch.float16),
+     ((1, 32, 1, 63), torch.float16), ((1, 32, 1, 64), torch.float32)],
+)
+@pytest.mark.parametrize("api", ["paged_attention", "paged_attention_batch"])
+def test_rejects_invalid_queries(device, shape, dtype, api):
+    """The reference's query checks (tests/unit/test_attention.py:353-368) on a gfx950 pool,
+    through both entry points: ValueError("query must be FP16 ..."), raised before any launch,
+    with the allocator's counts, table and length unchanged."""
+    allocator, request = _one_token_cache(device)
+    before = (allocator.capacity(), allocator.block_table(request), allocator.cached_length(request))
+    query = torch.zeros(shape, dtype=dtype, device=device)
+    with pytest.raises(ValueError, match="query must be FP16"):
+        if api == "paged_attention":
+            paged_attention(query, allocator, request, layer_index=0)
+        else:
+            paged_attention_batch(query, allocator, (request,), layer_index=0)
+    assert (allocator.capacity(), allocator.block_table(request), allocator.cached_length(request)) == before
+
+
+@pytest.mark.parametrize("layer", [-1, 22, True, 1.0])
+@pytest.mark.parametrize("api", ["paged_attention", "paged_attention_batch"])
+def test_rejects_invalid_layers(device, layer, api):
+    """tests/unit/test_attention.py:371-376 on a gfx950 pool: a layer index that is not an
+    int in [0, 22) (bool and float included) raises ValueError naming layer_index."""
+    allocator, request = _one_token_cache(device)
+    before = allocator.capacity()
+    query = torch.zeros(1, 32, 1, 64, dtype=torch.float16, device=device)
+    with pytest.raises(ValueError, match="layer_index"):
+        if api == "paged_attention":
+            paged_attention(query, allocator, request, layer_index=layer)
+        else:
+            paged_attention_batch(query, allocator, (request,), layer_index=layer)
+    assert allocator.capacity() == before
+
+
+@pytest.mark.parametrize("api", ["paged_attention", "paged_attention_batch"])
+def test_rejects_a_query_on_another_device(device, api):
+    """tests/unit/test_attention.py:379-384 on a gfx950 pool: a host query (the pool is on
+    the GPU) raises ValueError("... same device"), with the counts unchanged; the same
+    query on the pool's device then succeeds."""
+    allocator, request = _one_token_cache(device)
+    before = allocator.capacity()
+    for query in (torch.zeros(1, 32, 1, 64, dtype=torch.float16),
+                  torch.empty(1, 32, 1, 64, dtype=torch.float16, device="meta")):
+        with pytest.raises(ValueError, match="same device"):
+            if api == "paged_attention":
+                paged_attention(query, allocator, request, layer_index=0)
+            else:
+                paged_attention_batch(query, allocator, (request,), layer_index=0)
+        assert allocator.capacity() == before
+    good = torch.zeros(1, 32, 1, 64, dtype=torch.float16, device=device)
+    out = paged_attention(good, allocator, request, layer_index=0)
+    assert out.device == good.device and torch.equal(out, torch.zeros_like(out))  # V = 0 everywhere
 
 
 def test_batched_api_matches_single_request_api(device):
@@ -585,11 +639,6 @@ def test_batched_api_matches_single_request_api(device):
         assert torch.equal(single, batched[row : row + 1])
 
 
-def _flags_clear(workspace) -> bool:
-    """Every partial slot's ready flag (4 bytes at offset 2112 of each 2176-byte slot) is
-    zero: the state each call must leave for the next."""
-    slots = workspace.numel() // 2176
-    return not workspace[: slots * 2176].view(slots, 2176)[:, 2112:2116].any().item()
 
 
 def _permuted_tables(lengths, num_blocks, seed):
@@ -632,7 +681,7 @@ def test_long_sequences_cut_over_many_bins(device, lengths, num_blocks):
         _hip.paged_decode_attention(out, queries, pool, layer, torch.from_numpy(tables).to(device),
                                     torch.from_numpy(lengths).to(device), workspace=workspace)
         torch.cuda.synchronize()
-        assert _flags_clear(workspace)
+        assert flags_clear(workspace)
         outs.append(out)
     assert torch.equal(outs[0], outs[1])
     worst = Worst(f"long sequences {lengths.tolist()}")
@@ -696,6 +745,7 @@ def test_bad_block_in_a_cut_sequence_poisons_only_its_row(device, where):
     workspace = torch.zeros(_hip.workspace_bytes(w.batch, w.tables.shape[1]), dtype=torch.uint8, device=device)
     good = torch.empty_like(queries)
     _hip.paged_decode_attention(good, queries, pool, 6, torch.from_numpy(w.tables).to(device), lens, workspace=workspace)
+    assert fault_word(workspace) == 0
     broken = w.tables.copy()
     broken[b, j0 + n // 2] = w.num_blocks + 3
     bad = torch.empty_like(queries)
@@ -705,7 +755,8 @@ def test_bad_block_in_a_cut_sequence_poisons_only_its_row(device, where):
     others = [x for x in range(w.batch) if x != b]
     assert torch.equal(bad[others], good[others])
     assert not torch.isnan(good).any()
-    assert _flags_clear(workspace)
+    assert flags_clear(workspace)
+    assert fault_word(workspace) == _hip.FAULT_BLOCK_ID
 
 
 def _spans(plan):
@@ -720,13 +771,19 @@ def _spans(plan):
     return spans
 
 
-@pytest.mark.parametrize("fault", ["missing earlier part", "slots outside the workspace", "sequence outside the batch"])
+@pytest.mark.parametrize(
+    "fault", ["missing earlier part", "missing merging part", "slots outside the workspace", "sequence outside the batch"]
+)
 def test_malformed_plans_stay_in_bounds_and_spoil_only_their_rows(device, fault):
     """Plans that do not match the batch: a cut sequence whose earlier part's row was
-    dropped (its merge waits out its bounded spin and writes NaN), a cut sequence whose
-    partial slots point past the workspace (neither stored nor merged: its row is left
-    alone), a complete sequence relabelled past the batch (not written). Every other row
-    keeps the bits of the intact plan, and the part flags end at zero."""
+    dropped (its merge waits out its bounded spin, writes NaN and records
+    PC_ATTN_FAULT_MERGE_TIMEOUT, which the fault check turns into AttentionFaultError), a cut
+    sequence whose merging row was dropped (its earlier parts' flags stay raised; the row is
+    never written), a cut sequence whose partial slots point past the workspace (neither
+    stored nor merged: its row is left alone), a complete sequence relabelled past the batch
+    (not written). Every other row keeps the bits of the intact plan. The part flags end at
+    zero, except those of the dropped merge: a later call with a new plan on the same
+    workspace ignores them (they carry the old plan's epoch) and gives the intact plan's bits."""
     w = workloads.batched_decode(batch=64, num_blocks=8192, seed=86)
     plan = _hip.decode_plan(w.lengths, w.tables)
     spans = _spans(plan)
@@ -739,12 +796,32 @@ def test_malformed_plans_stay_in_bounds_and_spoil_only_their_rows(device, fault)
     good = torch.full_like(queries, 7.0)
     _hip.paged_decode_attention(good, queries, pool, 8, tables, lens, workspace=workspace)
     bad_plan = plan.copy()
+    merger_dropped = set()
     if fault == "missing earlier part":
         b = min(spans)
         row = spans[b][0][0]
         bad_plan[row] = 0  # the whole bin is dropped: every sequence it touches is spoiled
         spoiled = {int(x) for x in plan[row, 8 : 8 + 8 * int(plan[row, 0]) : 8]}
         nan_rows = {x for x in spoiled if x in spans}
+    elif fault == "missing merging part":
+        # a sequence whose merging bin holds no earlier part of another sequence, so that no
+        # merge times out and the flags it leaves raised meet the next call
+        def merging_row(x):
+            return spans[x][max(spans[x])][0]
+
+        def ends_with_earlier_part(row):
+            last = 8 + 8 * (int(plan[row, 0]) - 1)
+            return plan[row, last + 6] > 1 and plan[row, last + 5] < plan[row, last + 6] - 1
+
+        b = min((x for x in spans if not ends_with_earlier_part(merging_row(x))), default=min(spans))
+        row = merging_row(b)  # the bin holding the sequence's last part
+        bad_plan[row] = 0
+        spoiled = {int(x) for x in plan[row, 8 : 8 + 8 * int(plan[row, 0]) : 8]}
+        # sequences whose merging part was in the dropped bin: their earlier parts stay flagged
+        merger_dropped = {x for x in spoiled if x in spans and spans[x][max(spans[x])][0] == row}
+        assert b in merger_dropped
+        # an earlier part of another sequence in the dropped bin makes that sequence's merge time out
+        nan_rows = {x for x in spoiled if x in spans and x not in merger_dropped}
     elif fault == "slots outside the workspace":
         b = min(spans)
         for row, s, _, _, _ in spans[b].values():
@@ -769,7 +846,67 @@ def test_malformed_plans_stay_in_bounds_and_spoil_only_their_rows(device, fault)
     assert torch.equal(bad[others], good[others])
     for x in nan_rows:
         assert torch.isnan(bad[x]).all(), x
-    if fault != "missing earlier part":
-        for x in spoiled:
-            assert torch.equal(bad[x], torch.full_like(bad[x], 7.0)), x  # never written
-    assert _flags_clear(workspace)
+    for x in spoiled - nan_rows if fault != "missing earlier part" else ():
+        assert torch.equal(bad[x], torch.full_like(bad[x], 7.0)), x  # never written
+    raised = int((workspace_flags(workspace) != 0).sum().item())
+    if merger_dropped:
+        assert raised > 0, "the dropped merge's earlier parts should still be flagged"
+        _say("flags left raised by the dropped merge:", raised)
+    else:
+        assert raised == 0
+    expected_fault = _hip.FAULT_MERGE_TIMEOUT if nan_rows else 0
+    assert fault_word(workspace) == expected_fault
+    if expected_fault:
+        with pytest.raises(_hip.AttentionFaultError, match="bounded wait"):
+            _hip.check_attention_faults(workspace, "test")
+        assert fault_word(workspace) == 0 and flags_clear(workspace)  # zeroed whole
+    if merger_dropped:
+        # a new plan (new epoch) of the same batch on the same workspace: the old flags are not taken
+        again = torch.full_like(queries, 7.0)
+        _hip.paged_decode_attention(again, queries, pool, 8, tables, lens, workspace=workspace)
+        torch.cuda.synchronize()
+        assert torch.equal(again, good)
+        assert fault_word(workspace) == 0
+    assert flags_clear(workspace)
+
+
+@pytest.mark.parametrize("stale", ["earlier epoch", "other layer"])
+def test_stale_raised_flags_are_not_taken(device, stale):
+    """Flags left raised in the workspace by an earlier call (planted here from the host in
+    every partial slot, with garbage partials: an earlier plan's epoch, or this plan's epoch
+    and another layer, with every XCD id) are never taken for this call's parts: the output
+    equals a call on a clean workspace bit for bit, no fault is recorded, and every flag ends
+    at zero."""
+    w = workloads.batched_decode(batch=64, num_blocks=8192, seed=87)
+    plan = _hip.decode_plan(w.lengths, w.tables)
+    assert _spans(plan)
+    epoch, layer = int(plan[0, 2]), 5
+    pool = _random_pool(device, w.num_blocks, 23)
+    queries = torch.from_numpy(w.queries(layer)).to(device)
+    lens = torch.from_numpy(w.lengths).to(device)
+    tables = torch.from_numpy(w.tables).to(device)
+    device_plan = torch.from_numpy(plan).to(device)
+    nbytes = _hip.workspace_bytes(w.batch, w.tables.shape[1])
+    clean = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    expected = torch.full_like(queries, 7.0)
+    _hip.paged_decode_attention(expected, queries, pool, layer, tables, lens, plan=device_plan, workspace=clean)
+    planted = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=device,
+                            generator=torch.Generator(device=device).manual_seed(88))
+    planted[:256] = 0  # the fault word starts clear
+    slots = (nbytes - 256) // 2176
+    if stale == "earlier epoch":
+        key = (((epoch - 1) & ((1 << 22) - 1)) << 9) | (layer << 4)
+    else:
+        key = (epoch << 9) | (((layer + 1) % 22) << 4)
+    xcc = torch.arange(slots, dtype=torch.int32, device=device) % 8 + 1
+    flags = (key | xcc).view(torch.uint8).view(slots, 4)
+    planted[256 : 256 + slots * 2176].view(slots, 2176)[:, 2112:2116] = flags
+    assert (workspace_flags(planted) != 0).all()
+    got = torch.full_like(queries, 7.0)
+    _hip.paged_decode_attention(got, queries, pool, layer, tables, lens, plan=device_plan, workspace=planted)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), expected.view(torch.int16))
+    assert fault_word(planted) == 0 and fault_word(clean) == 0
+    # the slots the plan uses were consumed and lowered; the others keep their planted flags
+    used = check_decode_plan(plan, w.lengths, w.tables, w.num_blocks, nbytes)["slots"]
+    assert int((workspace_flags(planted) == 0).sum().item()) == used * 4

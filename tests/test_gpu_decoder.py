@@ -341,10 +341,13 @@ def test_decode_paged_rows_do_not_depend_on_batch_composition(device):
                     torch.testing.assert_close(actual_kv, expected_kv, atol=0, rtol=0)
 
 
-def test_decode_paged_failure_discards_the_step(device, monkeypatch):
-    """A failure inside the step (here: attention of layer 3) leaves lengths, tables, counts
-    and every published slot unchanged, and the step can be retried
-    (tests/unit/test_decoder.py:298-360)."""
+@pytest.mark.parametrize("failure", ["raised", "device fault"])
+def test_decode_paged_failure_discards_the_step(device, monkeypatch, failure):
+    """A failure inside the step (attention of layer 3 raising, or reporting a device fault
+    through its workspace's fault word, forced from the host here, which the step reads
+    before it commits) leaves lengths, tables, counts and every published slot unchanged,
+    and the step can be retried (tests/unit/test_decoder.py:298-360). The device fault
+    surfaces as AttentionFaultError and leaves the workspace zeroed."""
     weights = _synthetic(device)
     pool = torch.full((22, 2, 6, 16, 4, 64), float("nan"), dtype=torch.float16, device=device)
     allocator = KVAllocator(pool)
@@ -356,20 +359,29 @@ def test_decode_paged_failure_discards_the_step(device, monkeypatch):
     tables = [allocator.block_table(request) for request in requests]
     published = pool.clone()
     calls = 0
-    original = dec.paged_attention_batch
+    original = dec.attend_rows
+    faulted = []
 
     def failing(*args, **kwargs):
         nonlocal calls
         calls += 1
         if calls == 4:
-            raise RuntimeError("injected decode failure")
+            if failure == "raised":
+                raise RuntimeError("injected decode failure")
+            out, workspace = original(*args, **kwargs)
+            _hip.fault_word(workspace).fill_(_hip.FAULT_FOREIGN_XCD)  # as a merge would record it
+            faulted.append(workspace)
+            return out, workspace
         return original(*args, **kwargs)
 
     tokens = torch.tensor([[3], [4]], device=device)
-    monkeypatch.setattr(dec, "paged_attention_batch", failing)
-    with pytest.raises(RuntimeError, match="injected"):
+    monkeypatch.setattr(dec, "attend_rows", failing)
+    expected = (RuntimeError, "injected") if failure == "raised" else (_hip.AttentionFaultError, "another XCD")
+    with pytest.raises(expected[0], match=expected[1]):
         dec.decode_paged(tokens, weights, allocator, requests)
-    monkeypatch.setattr(dec, "paged_attention_batch", original)
+    monkeypatch.setattr(dec, "attend_rows", original)
+    for workspace in faulted:
+        assert not workspace.any().item()  # zeroed by the fault check
     assert allocator.capacity() == counts
     assert [allocator.block_table(request) for request in requests] == tables
     for request, length in zip(requests, (15, 16)):

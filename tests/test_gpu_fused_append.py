@@ -21,6 +21,7 @@ import torch
 from pagedcore_amd import _hip
 from tests import workloads
 from tests.bin_plan import check_decode_plan, regrouped_plan
+from tests.support import fault_word, flags_clear, workspace_flags
 
 pytestmark = pytest.mark.gpu
 
@@ -53,9 +54,6 @@ def _slots(lengths, tables):
     return slots
 
 
-def _flags_clear(workspace) -> bool:
-    slots = workspace.numel() // 2176
-    return not workspace[: slots * 2176].view(slots, 2176)[:, 2112:2116].any().item()
 
 
 def _fp64_rows(pool, layer, tables, lengths, queries):
@@ -150,7 +148,7 @@ def test_fused_append_matches_append_then_attention(device, case):
         tables = _tables(lengths, num_blocks, 94)
     a, b, workspace, queries = _both_ways(device, lengths, tables, num_blocks, layer=9, seed=95)
     _assert_same(a, b, case)
-    assert _flags_clear(workspace)
+    assert flags_clear(workspace)
     nonempty = np.flatnonzero(np.asarray(lengths) > 0)
     assert torch.isfinite(b[1][torch.from_numpy(nonempty).to(device)]).all()
 
@@ -167,13 +165,38 @@ def test_fused_rows_match_fp64_after_append(device):
     assert error <= ATOL
 
 
+def test_long_context_b256_fused_at_full_size(device):
+    """The long-context workload exactly as the benchmark times it: batch 256, every sequence
+    2047 cached tokens + the new one (128 blocks each) in a fully shuffled 40000-block pool
+    (7.2e9 elements), the new rows appended by the fused call (pc_kv_append_paged_decode_attn)
+    on one copy of the pool and by pc_kv_append + pc_paged_decode_attn on another. Layer 21,
+    so the fused call's pool stores land at element offsets above 2^31. Both pools are
+    bit-equal (every layer, every block, every slot), all 256 output rows are bit-equal, and
+    every fused row is within 2e-3 of FP64 attention over the appended history."""
+    w = workloads.batched_decode(batch=256, num_blocks=40000, fixed_length=2048, seed=20261204)
+    layer = 21
+    slots = _slots(w.lengths, w.tables)
+    assert (slots // 16 == w.tables[:, 127]).all() and (slots % 16 == 15).all()
+    assert ((2 * layer + 1) * w.num_blocks + int(w.tables[:, 127].max())) * 4096 > 2**31
+    _say("b256 x 2048 fused at full size, layer", layer)
+    a, b, workspace, queries = _both_ways(device, w.lengths, w.tables, w.num_blocks, layer=layer, seed=100)
+    _assert_same(a, b, "b256 x 2048")
+    assert flags_clear(workspace) and fault_word(workspace) == 0
+    (pool, out) = b
+    del a
+    expected = _fp64_rows(pool, layer, w.tables, w.lengths, queries)
+    error = (out.cpu().double() - expected).abs().max().item()
+    _say(f"b256 fused rows vs fp64: max error {error:.2e}")
+    assert error <= ATOL
+
+
 def test_fused_append_with_regrouped_bins(device):
     """The plan's groups of bins moved to other XCDs: the same bits as the unfused pair."""
     w = workloads.batched_decode(batch=64, num_blocks=8192, seed=98)
     plan = regrouped_plan(_hip.decode_plan(w.lengths, w.tables), np.random.default_rng(4).permutation(8))
     a, b, workspace, _ = _both_ways(device, w.lengths, w.tables, w.num_blocks, layer=0, seed=99, plan=plan)
     _assert_same(a, b, "regrouped")
-    assert _flags_clear(workspace)
+    assert flags_clear(workspace)
 
 
 @pytest.mark.parametrize("where", ["last block", "earlier block"])
@@ -261,7 +284,7 @@ def test_fused_call_in_a_graph_replays_as_eager(device):
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), eager_out.view(torch.int16)), f"replay {replay}"
         assert torch.equal(pool.view(torch.int16), eager_pool.view(torch.int16)), f"replay {replay}"
-        assert _flags_clear(workspace)
+        assert flags_clear(workspace)
         call()  # eager work between replays
         torch.cuda.synchronize()
 
@@ -311,7 +334,7 @@ def test_fused_call_with_malformed_plans_writes_only_planned_rows(device, fault)
         _hip.planned_decode_attention(out, queries, target, 8, lens, torch.from_numpy(p).to(device), width, workspace,
                                       new_key=key, new_value=value)
         torch.cuda.synchronize()
-        assert _flags_clear(workspace)
+        assert flags_clear(workspace)
         results.append((target, out))
     (good_pool, good), (bad_pool, bad) = results
     others = [x for x in range(w.batch) if x not in spoiled]

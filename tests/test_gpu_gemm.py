@@ -112,7 +112,7 @@ def _sum_in_split_order(parts: torch.Tensor) -> torch.Tensor:
     return total.half()
 
 
-@pytest.mark.parametrize("rows,splits", [(128, 4), (64, 8), (3, 1)])
+@pytest.mark.parametrize("rows,splits", [(128, 4), (64, 8), (3, 1), (128, 16), (7, 64)])
 def test_add_rms_norm_parts_equals_the_fp16_path(device, rows, splits):
     gen = torch.Generator(device=device).manual_seed(rows * splits)
     width = 2048
@@ -129,7 +129,7 @@ def test_add_rms_norm_parts_equals_the_fp16_path(device, rows, splits):
     assert np.array_equal(_bits(out1), _bits(out2))
 
 
-@pytest.mark.parametrize("tokens,splits", [(128, 4), (5, 8)])
+@pytest.mark.parametrize("tokens,splits", [(128, 4), (5, 8), (128, 16), (3, 64)])
 def test_rope_kv_append_parts_equals_the_fp16_path(device, tokens, splits):
     gen = torch.Generator(device=device).manual_seed(tokens + splits)
     parts = torch.randn((splits, tokens, 2560), device=device, generator=gen) * 0.5

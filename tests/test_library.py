@@ -42,12 +42,13 @@ def _slots_bound(batch, max_blocks):
 
 def test_workspace_and_capacity_formulas():
     lib = _hip.load()
-    # one partial slot per (cut part, kv head): fp32 O of 8 q heads x 64 dims (2 KiB), then
-    # (max, sum) of the 8 q heads, then the part's ready flag, padded to 17 128-byte lines
+    # a 256-byte header (the fault word), then one partial slot per (cut part, kv head): fp32
+    # O of 8 q heads x 64 dims (2 KiB), then (max, sum) of the 8 q heads, then the part's
+    # ready flag, padded to 17 128-byte lines
     slot = 2048 + 64 + 64
-    assert slot == 2176
+    assert slot == 2176 and _hip.WORKSPACE_HEADER_BYTES == 256
     for batch, blocks in ((64, 128), (1, 9), (1, 10), (256, 128), (97, 128), (0, 128)):
-        assert lib.pc_attn_workspace_bytes(batch, blocks) == _slots_bound(batch, blocks) * 4 * slot
+        assert lib.pc_attn_workspace_bytes(batch, blocks) == 256 + _slots_bound(batch, blocks) * 4 * slot
         group = max(256, -(-batch * blocks // 256)) + 1 + (batch + 2) // 3 + 1
         assert lib.pc_attn_plan_capacity(batch, blocks) == 8 * group
     assert lib.pc_attn_workspace_bytes(64, 128) < 3 << 20  # a few MiB, independent of context length

@@ -221,6 +221,9 @@ def test_decode_steps_replay_the_smallest_graph_that_holds_the_batch(monkeypatch
             used.append((self.batch, len(rids)))
             return model.decode(tokens, None, self.allocator, rids)
 
+        def check_faults(self):
+            pass
+
     monkeypatch.setattr(decoder, "DecodeGraph", RecordingGraph)
     allocator = cpu_allocator(torch.zeros((22, 2, 32, 16, 4, 64), dtype=torch.float16))
     worker = DecodeWorker(None, allocator, max_active=5, prefill=model.prefill, decode=model.decode, graph_batch=(4, 2))
@@ -280,3 +283,53 @@ def test_admissions_replay_the_smallest_prefill_graph_that_holds_the_prompt(monk
     for bad in ((0,), (2049,), (True,), (16.0,)):
         with pytest.raises(ValueError, match="prefill graph sizes"):
             DecodeWorker(None, allocator, prefill=model.prefill, decode=model.decode, prefill_graph_tokens=bad)
+
+
+@pytest.mark.parametrize("where", ["graph", "eager"])
+def test_a_device_fault_stops_the_worker_before_it_emits(monkeypatch, where):
+    """A decode step whose paged attention reports a device fault (DecodeGraph.check_faults
+    after the tokens are fetched, or decode_paged's own check) raises AttentionFaultError
+    before any of that step's tokens is emitted; the worker then stops: every later step()
+    raises RuntimeError and nothing more is prefilled or decoded (fail closed)."""
+    from pagedcore_amd import decoder
+    from pagedcore_amd._hip import FAULT_MERGE_TIMEOUT, AttentionFaultError
+
+    model = ScriptedModel()
+    steps = []
+
+    def faulty_decode(tokens, weights, allocator, rids):
+        steps.append(len(rids))
+        logits = model.decode(tokens, weights, allocator, rids)
+        if len(steps) == 3 and where == "eager":
+            raise AttentionFaultError(FAULT_MERGE_TIMEOUT, "decode_paged")
+        return logits
+
+    class FaultyGraph:
+        def __init__(self, weights, allocator, batch):
+            self.allocator = allocator
+
+        def step(self, tokens, rids):
+            return faulty_decode(tokens, None, self.allocator, rids)
+
+        def check_faults(self):
+            if len(steps) == 3:
+                raise AttentionFaultError(FAULT_MERGE_TIMEOUT, "DecodeGraph.step")
+
+    monkeypatch.setattr(decoder, "DecodeGraph", FaultyGraph)
+    allocator = cpu_allocator(torch.zeros((22, 2, 32, 16, 4, 64), dtype=torch.float16))
+    worker = DecodeWorker(None, allocator, max_active=3, prefill=model.prefill, decode=faulty_decode,
+                          graph_batch=(4,) if where == "graph" else None)
+    _submit(worker, model, [_request(f"r{i}", new=8) for i in range(4)])
+    emitted = worker.step() + worker.step()
+    assert len(emitted) == 2 + 3  # r0's prefill and decode tokens; r1's prefill token, both decode tokens
+    with pytest.raises(AttentionFaultError, match="bounded wait"):
+        worker.step()
+    assert worker.fault is not None and worker.fault.faults == FAULT_MERGE_TIMEOUT
+    prefills = list(model.prefills)
+    for _ in range(2):
+        with pytest.raises(RuntimeError, match="stopped after a device fault"):
+            worker.step()
+    assert len(steps) == 3 and model.prefills == prefills  # nothing launched after the fault
+    # no token of the faulted step was selected: each request holds its prefill token and
+    # the decode tokens of the steps before the fault
+    assert {rid: len(state.selected) for rid, state in worker._active.items()} == {"r0": 3, "r1": 2, "r2": 1}
