@@ -211,9 +211,9 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_word_kernel(
 // last is stored by its bin, which then raises the part's flag (after the stores are
 // acknowledged); the bin holding the last part (dispatched after all the others, so waiting
 // cannot deadlock) stages each part in LDS as its flag rises, combines them in span order
-// with its own last (their max first, then the weighted sums), writes the output and lowers
-// the flags. Partials and flags stay in the XCD's L2 (plain
-// stores and loads are coherent there); the flag carries the plan's epoch, the layer and
+// with its own last (their max first, then the weighted sums), lowers the flags and writes
+// the output rows from registers. Partials and flags stay in the XCD's L2 (plain stores and
+// loads are coherent there); the flag carries the plan's epoch, the layer and
 // the writer's XCD id: a flag of another epoch or layer is not this call's and is waited
 // past, and a merge that sees this call's flag with another XCD's id writes NaN rows
 // instead of reading stale partials and records the fault in the workspace.
@@ -327,7 +327,8 @@ __device__ __forceinline__ void fold_part(Part& acc, const Part& p) {
   }
 }
 
-// fp16 output rows [8 q heads][64] of a partial, normalized, in natural order into `area`.
+// fp16 output rows [8 q heads][64] of a partial, normalized, in natural order into `area`
+// (LDS or the output rows themselves).
 __device__ __forceinline__ void put_output(char* area, int lane, const Part& p) {
   const int c = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -748,7 +749,7 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
     }
   }
   // The last part of a cut sequence: wait for the other parts' flags, fold them in span
-  // order and this bin's part last, write the rows, lower the flags. This code stays small
+  // order and this bin's part last, lower the flags, write the rows. This code stays small
   // and its loops rolled: it runs once per merge, cold in the instruction cache, where every
   // 64-byte line fetched costs an L2 round trip.
   // A block id outside the pool anywhere in the bin (lane L of vector k holds id 64 k + L).
@@ -839,16 +840,14 @@ __global__ __launch_bounds__(kBinThreads) void paged_decode_bin_kernel(const int
       }
       fault |= (timeout ? PC_ATTN_FAULT_MERGE_TIMEOUT : 0) | (foreign ? PC_ATTN_FAULT_FOREIGN_XCD : 0);
     }
-    if (b0 >= 0 && b0 < batch) {
-      wave_lds_fence();
-      put_output(ring, lane, acc_p);  // the ring is free after the stream
-      wave_lds_fence();
-      *reinterpret_cast<uint4*>(out + (static_cast<int64_t>(b0) * kQHeads + kGroup * h) * kHeadDim + lane * 8) =
-          *reinterpret_cast<const uint4*>(ring + lane * 16);
-    }
     for (int k = lane; k < nspan0 - 1; k += 64) {
       __hip_atomic_store(reinterpret_cast<int32_t*>(part_slot(slots, slot0, k, h) + kFlagOffset), 0, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (b0 >= 0 && b0 < batch) {
+      // Straight from registers (16 lanes per 32-byte run of a row): no LDS round trip.
+      put_output(reinterpret_cast<char*>(out + (static_cast<int64_t>(b0) * kQHeads + kGroup * h) * kHeadDim), lane,
+                 acc_p);
     }
   }
   // `fault` is uniform over the wave; one lane ORs it into the fault word.
