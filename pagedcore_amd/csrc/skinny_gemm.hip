@@ -316,11 +316,17 @@ int pc_gemm_m128(void* out, const void* x, const void* w, int32_t m, int32_t n, 
     case kPartials:
     case kHalf:
       if (epilogue == kHalf && splits != 1) return set_error(PC_ERR_ARGUMENT, "fp16 output needs one split");
-      // 64-row tiles with eight waves when they alone fill the GPU's workgroup slots, else
-      // 32-row tiles with four waves.
+      // 64-row tiles with eight waves when they alone fill the GPU's workgroup slots; with
+      // four waves (2 x 4 register tiles per wave) when they give 160 to 175 workgroups, where
+      // 32-row tiles would need more workgroups than one round on the CUs (q|k|v at 4
+      // splits: 7.5 vs 8.3 us); else 32-row tiles with four waves.
       if (n % 64 == 0 && (n / 64) * splits >= 176) {
         a.tiles = n / 64;
         return epilogue == kHalf ? launch<64, 64, 4, 8, kHalf>(a, splits, s) : launch<64, 64, 4, 8, kPartials>(a, splits, s);
+      }
+      if (n % 64 == 0 && (n / 64) * splits >= 160 && (n / 32) * splits > 256) {
+        a.tiles = n / 64;
+        return epilogue == kHalf ? launch<64, 64, 4, 4, kHalf>(a, splits, s) : launch<64, 64, 4, 4, kPartials>(a, splits, s);
       }
       if (n % 32 != 0) return set_error(PC_ERR_ARGUMENT, "n = %d must be a multiple of 32", n);
       a.tiles = n / 32;
