@@ -219,6 +219,17 @@ _CountingDict = _counting(
 )
 
 
+def _upload(array: np.ndarray, device: torch.device) -> Tensor:
+    """A host array on `device`. For a GPU the copy goes through pinned memory and is
+    enqueued on the current stream without blocking the host (a copy from pageable memory
+    would wait for the stream to drain); torch keeps the pinned buffer until the copy has
+    run, and every consumer is ordered after it on the same stream."""
+    tensor = torch.from_numpy(np.ascontiguousarray(array))
+    if device.type != "cuda":
+        return tensor.to(device)
+    return tensor.pin_memory().to(device, non_blocking=True)
+
+
 def _slot_mapping(blocks: BlockTable, start: int, count: int) -> np.ndarray:
     """Pool slot (block * 16 + offset) of positions start .. start + count - 1."""
     positions = np.arange(start, start + count, dtype=np.int64)
@@ -377,7 +388,7 @@ class KVAllocator:
         blocks = sequence.blocks + new_blocks
         slots = _slot_mapping(blocks, sequence.length, tokens)
         positions = np.arange(sequence.length, length, dtype=np.int64)
-        both = torch.from_numpy(np.stack([slots, positions])).to(self._pool.device)
+        both = _upload(np.stack([slots, positions]), self._pool.device)
         staged = StagedPrompt(request_id, tokens, both[0], both[1])
         self._prompt_append = staged
         self._touch()
@@ -601,7 +612,7 @@ class KVAllocator:
             positions[row] = position
         if not self._pool.is_cuda:
             return slots, positions
-        both = torch.from_numpy(np.stack([slots, positions])).to(self._pool.device)
+        both = _upload(np.stack([slots, positions]), self._pool.device)
         result = (both[0], both[1])
         self._decode_slot_cache[request_ids] = result
         return result
@@ -714,7 +725,7 @@ class KVAllocator:
         batch = self._gather(request_ids, layer_index)
         if batch.plan is None:
             plan = _hip.decode_plan(batch.host_lengths, batch.host_tables)
-            batch.plan = torch.from_numpy(plan).to(self._pool.device)
+            batch.plan = _upload(plan, self._pool.device)
         return batch.plan
 
     def _gather(self, request_ids: Sequence[RequestId], layer_index: int) -> _DecodeBatch:
@@ -743,8 +754,8 @@ class KVAllocator:
             lengths[row] = sequence.length
         appends = self._decode_appends or {}
         result = _DecodeBatch(
-            torch.from_numpy(tables).to(self._pool.device),
-            torch.from_numpy(lengths).to(self._pool.device),
+            _upload(tables, self._pool.device),
+            _upload(lengths, self._pool.device),
             tables,
             lengths,
             tuple(appends[request_id] for request_id in request_ids if request_id in appends),

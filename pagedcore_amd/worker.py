@@ -21,6 +21,16 @@ Everything runs on the allocator's worker thread and stream, so a release is ord
 every launch that read the released blocks (the reference's stream-ordered reuse rule,
 docs/DESIGN.md:282).
 
+The host waits for the GPU once per iteration. The admitted request's first token is
+selected on the device (argmax of the prefill's last logits) and fed to the decode step
+from device memory, and its host-side selection happens after the step, with the decode's
+tokens, in the order of the plan (the prefill token first): the decode step's host work
+then runs while the GPU executes the prefill. Only when that token can end the request
+early, an EOS with ignore_eos off, does the host wait for it before forming the batch, as
+the batch must not hold a finished request. Inputs go to the device through pinned memory
+without blocking, and the selected tokens come back with one asynchronous copy and one
+event wait.
+
 A device-side failure fails closed (the reference's rule for unsafe device failures,
 docs/DESIGN.md:178,255,282): when a decode step's paged attention reports a fault (its
 workspace's fault word, read right after the step's tokens are fetched and before any is
@@ -220,19 +230,59 @@ class DecodeWorker:
     def _iterate(self) -> List[Tuple[RequestId, int]]:
         self._cleanup()
         emitted: List[Tuple[RequestId, int]] = []
-        self._admit_one(emitted)
-        batch = tuple(rid for rid, state in self._active.items() if state.finish is None)
+        first = self._admit_one()  # (admitted request, its first token on the device)
+        if first is not None:
+            request = self._active[first[0]].request
+            if request.max_new_tokens > 1 and not request.ignore_eos:
+                # an EOS would finish it now, and a finished request must not be decoded
+                self._select(first[0], int(first[1]), emitted)
+                first = None
+        # A request admitted with one token to select is finished by that token.
+        batch = tuple(
+            rid
+            for rid, state in self._active.items()
+            if state.finish is None and (first is None or rid != first[0] or state.request.max_new_tokens > 1)
+        )
+        chosen: List[Tensor] = [] if first is None else [first[1].view(1)]
+        graph = None
         if batch:
-            tokens = torch.tensor(
-                [[self._active[rid].selected[-1]] for rid in batch], dtype=torch.int64, device=self._device()
-            )
+            tokens = self._batch_tokens(batch)
+            if first is not None and first[0] in batch:
+                tokens[batch.index(first[0]), 0] = first[1]  # the prefill's selection, device to device
             logits, graph = self._decode_batch(tokens, batch)
-            chosen = logits[:, -1].argmax(dim=-1).tolist()
-            if graph is not None:
-                graph.check_faults()  # decode_paged checks inside its step
-            for rid, token in zip(batch, chosen):
-                self._select(rid, int(token), emitted)
+            chosen.append(logits[:, -1].argmax(dim=-1))
+        values = self._fetch(torch.cat(chosen)) if chosen else []
+        if graph is not None:
+            graph.check_faults()  # decode_paged checks inside its step
+        if first is not None:
+            self._select(first[0], values[0], emitted)
+            values = values[1:]
+        for rid, token in zip(batch, values):
+            self._select(rid, token, emitted)
         return emitted
+
+    def _batch_tokens(self, batch: Tuple[RequestId, ...]) -> Tensor:
+        """int64 [len(batch), 1] on the pool's device: each request's last selected token (0
+        for one whose first token is still on the device), uploaded through pinned memory."""
+        host = torch.tensor(
+            [[self._active[rid].selected[-1] if self._active[rid].selected else 0] for rid in batch], dtype=torch.int64
+        )
+        device = self._device()
+        if device.type != "cuda":
+            return host.to(device)
+        return host.pin_memory().to(device, non_blocking=True)
+
+    def _fetch(self, values: Tensor) -> List[int]:
+        """Host copy of a small device int64 vector: one asynchronous copy to pinned memory
+        and a wait on an event recorded after it (other streams keep running)."""
+        if values.device.type != "cuda":
+            return [int(v) for v in values.tolist()]
+        host = torch.empty(values.shape, dtype=values.dtype, pin_memory=True)
+        host.copy_(values, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record()
+        done.synchronize()
+        return host.tolist()
 
     def run(self, max_steps: Optional[int] = None) -> Dict[RequestId, GreedyResult]:
         """Iterate until every submitted request finished (and was cleaned up)."""
@@ -258,25 +308,29 @@ class DecodeWorker:
         if self._cancelled:
             self._pending = deque(r for r in self._pending if r.request_id not in self._cancelled)
 
-    def _admit_one(self, emitted: List[Tuple[RequestId, int]]) -> None:
+    def _admit_one(self) -> Optional[Tuple[RequestId, Tensor]]:
+        """Admit and prefill the queue head if it fits; returns it with its first token
+        still on the device (argmax of the prompt's last logits), or None."""
         if not self._pending or len(self._active) >= self._max_active:
-            return
+            return None
         request = self._pending[0]
         counts = self._allocator.capacity()
         if request.block_credits > counts.total_blocks - counts.reserved_blocks:
-            return  # waits (strict FIFO: nothing behind it is admitted first)
+            return None  # waits (strict FIFO: nothing behind it is admitted first)
         self._pending.popleft()
         rid = request.request_id
         self._allocator.create(KVReservation(rid, request.block_credits))
         self._active[rid] = _Active(request)
         try:
-            ids = torch.tensor([list(request.input_ids)], dtype=torch.int64, device=self._device())
+            device = self._device()
+            ids = torch.tensor([list(request.input_ids)], dtype=torch.int64)
+            ids = ids.pin_memory().to(device, non_blocking=True) if device.type == "cuda" else ids.to(device)
             size = next((size for size in self._prompt_sizes if size >= len(request.input_ids)), None)
             if size is not None:
                 logits = self._prefill_graph_for(size).step(ids, rid)
             else:
                 logits = self._prefill(ids, self._weights, self._allocator, rid)
-            token = int(logits[0, -1].argmax())
+            token = logits[0, -1].argmax()
         except BaseException:
             # A failed admission leaves nothing behind: the request leaves the active set
             # and its reservation (with any blocks a partial prefill published) is
@@ -284,7 +338,7 @@ class DecodeWorker:
             self._active.pop(rid, None)
             self._allocator.release_all(rid)
             raise
-        self._select(rid, token, emitted)
+        return rid, token
 
     def _graph_for(self, size: int):
         graph = self._graphs.get(size)
