@@ -151,7 +151,10 @@ int64_t pc_attn_workspace_bytes(int32_t batch, int32_t max_blocks);
  * refused with PC_ERR_ARGUMENT before any HIP call (32 MiB covers, e.g., batch 4096 with
  * 128-block tables, but not batch 8192). The array starts at zero when the library loads
  * and every call leaves its flags at zero. Its fault word is not readable by the caller:
- * a fault shows only as NaN rows. `stream` must belong to the current device.
+ * a fault shows only as NaN rows. A merge that gave up waiting (a malformed plan, or a part
+ * held back past the bounded wait) can leave a late part's flag raised: a call with a new
+ * plan never takes it (the plan's epoch differs), a replay of the same plan could, so after
+ * NaN rows build a new plan. `stream` must belong to the current device.
  * Every call on one GPU
  * shares that GPU's array: calls that overlap in time on one GPU (concurrent streams,
  * threads) race and give wrong rows; calls ordered on one stream are safe. Arguments and
