@@ -294,9 +294,15 @@ class KVAllocator:
             raise ValueError("reservation exceeds KV context capacity")
         if reservation.maximum_block_credits > counts.total_blocks - counts.reserved_blocks:
             raise RuntimeError("KV pool has insufficient unreserved blocks")
+        before = self._verified_counts()
         self._sequences[request_id] = _SequenceCache(reservation)
         self._touch()
-        self._assert_accounting()
+        credits = reservation.maximum_block_credits
+        self._recount(
+            before if type(credits) is int and 0 < credits <= MAX_BLOCKS_PER_REQUEST else None,
+            reserved=credits,
+            active=1,
+        )
 
     def capacity(self) -> CapacityCounts:
         """Snapshot ownership and credits, including requests awaiting cleanup."""
@@ -351,12 +357,13 @@ class KVAllocator:
         self._writer.append(self._pool, 0, key, value, _slot_mapping(blocks, sequence.length, key.shape[1]))
 
         # Publish valid positions only after the K and V writes have been issued.
+        before = self._verified_counts()
         if additional:
             del self._free_blocks[-additional:]
         self._block_owners.update((block, request_id) for block in new_blocks)
         self._sequences[request_id] = _SequenceCache(sequence.reservation, blocks, length)
         self._touch()
-        self._assert_accounting()
+        self._recount(before, moved=additional, tokens=key.shape[1])
 
     @contextmanager
     def append_prompt(self, request_id: RequestId, tokens: int) -> Iterator[StagedPrompt]:
@@ -396,11 +403,14 @@ class KVAllocator:
             yield staged
             if staged.written_layers != LAYERS:
                 raise RuntimeError("prompt append must write every cache layer before committing")
+            before = self._verified_counts()
+            if self._sequences.get(request_id) is not sequence:
+                before = None  # replaced from outside while staged: check everything
             if additional:
                 del self._free_blocks[-additional:]
             self._block_owners.update((block, request_id) for block in new_blocks)
             self._sequences[request_id] = _SequenceCache(sequence.reservation, blocks, length)
-            self._assert_accounting()
+            self._recount(before, moved=additional, tokens=tokens)
         finally:
             self._prompt_append = None
             self._touch()
@@ -783,12 +793,19 @@ class KVAllocator:
         """Release once on the worker stream; unknown/released requests raise KeyError."""
         self._check_mutation()
         self._assert_accounting()
+        before = self._verified_counts()
         sequence = self._sequences.pop(request_id)
         for block in sequence.blocks:
             del self._block_owners[block]
         self._free_blocks.extend(reversed(sequence.blocks))
         self._touch()
-        self._assert_accounting()
+        self._recount(
+            before,
+            moved=-len(sequence.blocks),
+            tokens=-sequence.length,
+            reserved=-sequence.reservation.maximum_block_credits,
+            active=-1,
+        )
 
     def _touch(self) -> None:
         self._version += 1
@@ -837,6 +854,33 @@ class KVAllocator:
     def _remember(self, counts: CapacityCounts) -> None:
         key = self._state_key()
         self._verified = None if key is None else (key, counts)
+
+    def _recount(
+        self, before: Optional[CapacityCounts], *, moved: int = 0, tokens: int = 0, reserved: int = 0, active: int = 0
+    ) -> None:
+        """Accounting after one of this allocator's own mutations. `before` is the verified
+        state it started from (None: not verified, or changed from outside since): then the
+        full check runs, as the reference does after every mutation. Otherwise the mutation
+        was one of the few this class makes, each of which keeps every invariant by
+        construction from a verified state (blocks leave the free-list tail for the request
+        that was checked to hold the credits, a released request's verified blocks return
+        to the free list, a new request starts empty within its checked credits), so the
+        counts move by exactly `moved` blocks from free to owned (negative: back), `tokens`
+        cached positions, `reserved` credits and `active` slots, and are remembered as
+        verified without rescanning the pool."""
+        if before is None:
+            self._assert_accounting()
+            return
+        self._remember(
+            CapacityCounts(
+                total_blocks=before.total_blocks,
+                free_blocks=before.free_blocks - moved,
+                owned_blocks=before.owned_blocks + moved,
+                reserved_blocks=before.reserved_blocks + reserved,
+                active_slots=before.active_slots + active,
+                live_cached_token_slots=before.live_cached_token_slots + tokens,
+            )
+        )
 
     def _assert_accounting(self) -> CapacityCounts:
         """Full ownership invariants (reference src/pagedcore/kv_cache.py:314-357).

@@ -9,6 +9,7 @@ the CpuCopyWriter test double; the GPU tests repeat the data checks on the HIP p
 from __future__ import annotations
 
 from concurrent.futures import ThreadPoolExecutor
+from contextlib import nullcontext
 from dataclasses import replace
 from math import ceil
 from typing import Any
@@ -23,7 +24,7 @@ from hypothesis.stateful import RuleBasedStateMachine, invariant, precondition, 
 from oracle import paged_reference as ref
 from pagedcore_amd.config import PagedCoreConfig
 from pagedcore_amd.engine_types import CapacityCounts, KVReservation, RequestId
-from pagedcore_amd.kv_cache import KVAllocator, allocate_kv_pool
+from pagedcore_amd.kv_cache import LAYERS, KVAllocator, allocate_kv_pool
 from tests.support import CpuCopyWriter, cpu_allocator, kv_values
 
 
@@ -685,6 +686,37 @@ class _AllocatorMachine(RuleBasedStateMachine):
         expected["blocks"] = table
         expected["tokens"].extend(tags)
 
+    @precondition(lambda self: bool(self.requests))
+    @rule(data=st.data(), tokens=st.sampled_from((1, 16, 17, 40)), complete=st.booleans())
+    def append_prompt(self, data, tokens, complete):
+        """The staged prompt append (the fused prefill path): the caller writes each layer's
+        K/V to the staged slots; published only when all 22 layers were recorded."""
+        request = data.draw(st.sampled_from(tuple(self.requests)), label="request")
+        expected = self.requests[request]
+        length = len(expected["tokens"]) + tokens
+        if length > expected["credits"] * 16:
+            with pytest.raises(RuntimeError, match="exceeds request reservation"):
+                with self.allocator.append_prompt(request, tokens):
+                    pass
+            return
+        tags = list(range(self.next_token, self.next_token + tokens))
+        self.next_token += tokens
+        key, value = _tagged_kv(tags)
+        with pytest.raises(RuntimeError, match="every cache layer") if not complete else nullcontext():
+            with self.allocator.append_prompt(request, tokens) as staged:
+                block, offset = staged.slot_mapping // 16, staged.slot_mapping % 16
+                for layer in range(LAYERS if complete else LAYERS - 1):
+                    self.pool[layer, 0, block, offset] = key[layer]
+                    self.pool[layer, 1, block, offset] = value[layer]
+                    staged.record_layer(layer)
+        if not complete:
+            return
+        table = self.allocator.block_table(request)
+        assert set(table[len(expected["blocks"]) :]) <= self.free
+        self.free.difference_update(table[len(expected["blocks"]) :])
+        expected["blocks"] = table
+        expected["tokens"].extend(tags)
+
     @rule(slot=st.integers(0, 3))
     def release(self, slot):
         request = RequestId(str(slot))
@@ -701,6 +733,8 @@ class _AllocatorMachine(RuleBasedStateMachine):
         reserved = sum(r["credits"] for r in self.requests.values())
         live = sum(len(r["tokens"]) for r in self.requests.values())
         assert self.allocator.capacity() == CapacityCounts(self.total, self.total - owned, owned, reserved, len(self.requests), live)
+        # the counts kept across the allocator's own mutations equal a full rescan
+        assert self.allocator._full_accounting() == self.allocator.capacity()
         assert set(self.allocator._free_blocks) == self.free
         for request, r in self.requests.items():
             assert self.allocator.block_table(request) == r["blocks"]
