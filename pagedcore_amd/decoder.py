@@ -328,8 +328,7 @@ def decode_paged(
     if input_ids.device != weights.embedding.device:
         raise ValueError("input_ids and weights must be on the same device")
     _check_weights(weights, "decode")
-    for request_id in request_ids:
-        allocator.cached_length(request_id)  # KeyError for an unknown request, as the reference
+    allocator.cached_lengths(request_ids)  # KeyError for an unknown request, as the reference
     _check_gpu(allocator, weights, "decode")
     with allocator.append_decode(request_ids):
         table = rope_table(allocator.pool.device)
@@ -497,8 +496,7 @@ class DecodeGraph:
         if not 1 <= rows <= self.batch:
             raise ValueError(f"this decode graph runs batches of 1 to {self.batch} requests")
         allocator = self._allocator
-        for request_id in request_ids:
-            allocator.cached_length(request_id)  # KeyError for an unknown request
+        allocator.cached_lengths(request_ids)  # KeyError for an unknown request
         with allocator.append_decode(request_ids):
             staged = allocator.staged_decode(request_ids, width=MAX_BLOCKS)
             turn = self._turn

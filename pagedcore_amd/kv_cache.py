@@ -319,6 +319,14 @@ class KVAllocator:
         self._assert_accounting()
         return self._sequences[request_id].length
 
+    def cached_lengths(self, request_ids: Sequence[RequestId]) -> Tuple[int, ...]:
+        """cached_length of each request, with the worker and accounting checks done once
+        for the batch; KeyError for the first unknown request."""
+        self._check_worker()
+        self._assert_accounting()
+        sequences = self._sequences
+        return tuple(sequences[request_id].length for request_id in request_ids)
+
     @torch.inference_mode()
     def append(self, request_id: RequestId, key: Tensor, value: Tensor) -> None:
         """Append rotated K and unrotated V, each FP16 [22, tokens, 4, 64].
@@ -648,16 +656,15 @@ class KVAllocator:
             width = widest
         elif widest > width:
             raise ValueError("staged block tables are wider than the requested width")
+        counts = np.fromiter((len(sequence.blocks) for sequence in sequences), dtype=np.int64, count=len(sequences))
+        flat = np.fromiter(chain.from_iterable(sequence.blocks for sequence in sequences), dtype=np.int32, count=int(counts.sum()))
         tables = np.zeros((len(sequences), width), dtype=np.int32)
-        lengths = np.empty(len(sequences), dtype=np.int32)
-        slots = np.empty(len(sequences), dtype=np.int64)
-        positions = np.empty(len(sequences), dtype=np.int64)
-        for row, sequence in enumerate(sequences):
-            tables[row, : len(sequence.blocks)] = sequence.blocks
-            lengths[row] = sequence.length
-            positions[row] = sequence.length - 1
-            logical_block, offset = divmod(sequence.length - 1, BLOCK_TOKENS)
-            slots[row] = sequence.blocks[logical_block] * BLOCK_TOKENS + offset
+        tables[np.arange(width) < counts[:, None]] = flat  # row-major: each row's blocks in order
+        lengths = np.fromiter((sequence.length for sequence in sequences), dtype=np.int32, count=len(sequences))
+        positions = lengths.astype(np.int64) - 1
+        # the new position's slot: block (position // 16) of the row's table, offset position % 16
+        rows = np.arange(len(sequences))
+        slots = tables[rows, positions // BLOCK_TOKENS].astype(np.int64) * BLOCK_TOKENS + positions % BLOCK_TOKENS
         return StagedDecode(slots, positions, lengths, tables)
 
     def record_decode_writes(self, request_ids: Sequence[RequestId], layers: int = LAYERS) -> None:
