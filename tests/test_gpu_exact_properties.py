@@ -1,0 +1,96 @@
+"""Size-independent properties of the paged decode attention that hold bit for bit, checked
+at the benchmark's full sizes (batch 64 over U{1..2048} on an 8192-block pool, and batch
+256 x 2048 on a 40,000-block pool), where the oracle would take minutes per row:
+
+- doubling V (one layer's V plane, in place) doubles every output exactly: softmax weights
+  do not depend on V, the fp16 products with V, the fp32 sums, the split-K partials and
+  their merge all scale by 2 without rounding, and fp16(2x) = 2 fp16(x) for results in the
+  normal range (an fp16 subnormal result may differ by its last unit, 2^-24);
+- swapping two kv heads' K and V in the pool, together with their two groups of eight
+  query heads, swaps the corresponding output heads exactly (each kv head is computed by
+  its own wave with the same arithmetic, and the plan does not depend on heads).
+
+The reference computes each head independently (src/pagedcore/attention.py:31-53), so both
+hold for it up to its own rounding; here they pin the index arithmetic of the head mapping
+and the exactness of the split-K merge on the full workloads.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+from pagedcore_amd import _hip
+from tests import workloads
+
+pytestmark = pytest.mark.gpu
+
+SUBNORMAL = 2.0**-14  # smallest normal fp16 magnitude
+WORKLOADS = {
+    "batch64": dict(batch=64, num_blocks=8192, seed=61),
+    "batch256x2048": dict(batch=256, num_blocks=40000, fixed_length=2048, seed=62),
+}
+
+
+def _say(*parts) -> None:
+    print("[exact]", *parts, file=sys.stderr, flush=True)
+
+
+@pytest.fixture
+def device():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    return torch.device("cuda:0")
+
+
+def _setup(device, name):
+    w = workloads.batched_decode(**WORKLOADS[name])
+    gen = torch.Generator(device=device).manual_seed(w.seed)
+    pool = torch.randn((22, 2, w.num_blocks, 16, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    layer = 7
+    queries = torch.from_numpy(w.queries(layer)).to(device)
+    tables = torch.from_numpy(w.tables).to(device)
+    lens = torch.from_numpy(w.lengths).to(device)
+    plan = torch.from_numpy(_hip.decode_plan(w.lengths, w.tables)).to(device)
+    return w, pool, layer, queries, tables, lens, plan
+
+
+def _attend(pool, layer, queries, tables, lens, plan):
+    out = torch.full_like(queries, float("nan"))
+    workspace = _hip.paged_decode_attention(out, queries, pool, layer, tables, lens, plan=plan)
+    torch.cuda.synchronize()
+    _hip.check_attention_faults(workspace, "exact properties")
+    return out
+
+
+@pytest.mark.parametrize("name", list(WORKLOADS))
+def test_doubling_v_doubles_every_output_exactly(device, name):
+    _say("doubling V", name)
+    w, pool, layer, queries, tables, lens, plan = _setup(device, name)
+    out = _attend(pool, layer, queries, tables, lens, plan)
+    pool[layer, 1].mul_(2)  # exact in fp16 for N(0, 1) values
+    doubled = _attend(pool, layer, queries, tables, lens, plan)
+    assert not torch.isnan(out).any()
+    expected = out * 2  # exact: no fp16 output is near the overflow threshold
+    normal = out.abs() >= SUBNORMAL
+    assert torch.equal(doubled[normal], expected[normal]), "a normal-range output is not exactly doubled"
+    tiny = (doubled[~normal].float() - expected[~normal].float()).abs()
+    assert tiny.numel() == 0 or float(tiny.max()) <= 2.0**-24
+    _say(name, "rows", w.batch, "subnormal outputs", int((~normal).sum()))
+
+
+@pytest.mark.parametrize("name", list(WORKLOADS))
+@pytest.mark.parametrize("heads", [(0, 3), (1, 2)])
+def test_swapping_kv_heads_swaps_output_heads_exactly(device, name, heads):
+    _say("swapping kv heads", heads, name)
+    h1, h2 = heads
+    w, pool, layer, queries, tables, lens, plan = _setup(device, name)
+    out = _attend(pool, layer, queries, tables, lens, plan)
+    order = list(range(4))
+    order[h1], order[h2] = h2, h1
+    pool[layer] = pool[layer][..., order, :].clone()
+    qorder = [8 * order[g] + i for g in range(4) for i in range(8)]
+    swapped = _attend(pool, layer, queries[:, qorder].contiguous(), tables, lens, plan)
+    assert torch.equal(swapped, out[:, qorder])
