@@ -8,9 +8,13 @@ at the benchmark's full sizes (batch 64 over U{1..2048} on an 8192-block pool, a
   normal range (an fp16 subnormal result may differ by its last unit, 2^-24);
 - swapping two kv heads' K and V in the pool, together with their two groups of eight
   query heads, swaps the corresponding output heads exactly (each kv head is computed by
-  its own wave with the same arithmetic, and the plan does not depend on heads).
+  its own wave with the same arithmetic, and the plan does not depend on heads);
+- doubling the queries and halving the keys (none of them subnormal after halving) changes
+  no score and so no output bit;
+- for the fused append + attention launch, doubling V and the new value rows doubles the
+  outputs and the written V rows and leaves the K rows as they were.
 
-The reference computes each head independently (src/pagedcore/attention.py:31-53), so both
+The reference computes each head independently (src/pagedcore/attention.py:31-53), so these
 hold for it up to its own rounding; here they pin the index arithmetic of the head mapping
 and the exactness of the split-K merge on the full workloads.
 """
@@ -94,3 +98,49 @@ def test_swapping_kv_heads_swaps_output_heads_exactly(device, name, heads):
     qorder = [8 * order[g] + i for g in range(4) for i in range(8)]
     swapped = _attend(pool, layer, queries[:, qorder].contiguous(), tables, lens, plan)
     assert torch.equal(swapped, out[:, qorder])
+
+
+@pytest.mark.parametrize("name", list(WORKLOADS))
+def test_doubling_q_and_halving_k_changes_no_bit(device, name):
+    """(2q)(k/2) = qk exactly when no k is an fp16 subnormal after halving: the scores, and
+    so every output bit, are those of the unscaled call (pins the Q and K paths)."""
+    _say("2q, k/2", name)
+    w, pool, layer, queries, tables, lens, plan = _setup(device, name)
+    key = pool[layer, 0]
+    floor = torch.where(key < 0, -(2.0**-13), 2.0**-13).to(torch.float16)
+    key.copy_(torch.where(key.abs() < 2.0**-13, floor, key))  # halving keeps every k normal
+    out = _attend(pool, layer, queries, tables, lens, plan)
+    key.mul_(0.5)
+    scaled = _attend(pool, layer, queries * 2, tables, lens, plan)
+    assert not torch.isnan(out).any()
+    assert torch.equal(scaled, out)
+
+
+@pytest.mark.parametrize("name", list(WORKLOADS))
+def test_fused_append_doubling_v_doubles_outputs_and_written_rows(device, name):
+    """The same for pc_kv_append_paged_decode_attn (the kernel the batch-256 figure times):
+    doubling the pool's V plane and the new value rows doubles every output and every
+    written V row, and the written K rows are unchanged."""
+    _say("fused doubling V", name)
+    w, pool, layer, queries, tables, lens, plan = _setup(device, name)
+    gen = torch.Generator(device=device).manual_seed(w.seed + 1)
+    new_key = torch.randn((w.batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    new_value = torch.randn((w.batch, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    twin = pool.clone()
+    twin[layer, 1].mul_(2)
+    outs = []
+    for p, v in ((pool, new_value), (twin, new_value * 2)):
+        out = torch.full_like(queries, float("nan"))
+        workspace = torch.zeros(_hip.workspace_bytes(w.batch, w.tables.shape[1]), dtype=torch.uint8, device=device)
+        _hip.planned_decode_attention(out, queries, p, layer, lens, plan, w.tables.shape[1], workspace,
+                                      new_key=new_key, new_value=v)
+        torch.cuda.synchronize()
+        _hip.check_attention_faults(workspace, "fused exact properties")
+        outs.append(out)
+    assert not torch.isnan(outs[0]).any()
+    normal = outs[0].abs() >= SUBNORMAL
+    assert torch.equal(outs[1][normal], (outs[0] * 2)[normal])
+    tiny = (outs[1][~normal].float() - (outs[0] * 2)[~normal].float()).abs()
+    assert tiny.numel() == 0 or float(tiny.max()) <= 2.0**-24
+    assert torch.equal(twin[layer, 0], pool[layer, 0])  # K planes, new rows included
+    assert torch.equal(twin[layer, 1], pool[layer, 1] * 2)  # V planes, new rows included
