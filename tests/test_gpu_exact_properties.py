@@ -12,7 +12,8 @@ at the benchmark's full sizes (batch 64 over U{1..2048} on an 8192-block pool, a
 - doubling the queries and halving the keys (none of them subnormal after halving) changes
   no score and so no output bit;
 - for the fused append + attention launch, doubling V and the new value rows doubles the
-  outputs and the written V rows and leaves the K rows as they were.
+  outputs and the written V rows and leaves the K rows as they were;
+- the first three also for the causal prompt attention kernel (pc_prefill_attention).
 
 The reference computes each head independently (src/pagedcore/attention.py:31-53), so these
 hold for it up to its own rounding; here they pin the index arithmetic of the head mapping
@@ -144,3 +145,45 @@ def test_fused_append_doubling_v_doubles_outputs_and_written_rows(device, name):
     assert tiny.numel() == 0 or float(tiny.max()) <= 2.0**-24
     assert torch.equal(twin[layer, 0], pool[layer, 0])  # K planes, new rows included
     assert torch.equal(twin[layer, 1], pool[layer, 1] * 2)  # V planes, new rows included
+
+
+# --- the prompt attention kernel (pc_prefill_attention) -----------------------------------
+
+
+def _prompt(device, tokens, seed):
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn((tokens, 32, 64), dtype=torch.float16, device=device, generator=gen)
+    k = torch.randn((tokens, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    v = torch.randn((tokens, 4, 64), dtype=torch.float16, device=device, generator=gen)
+    return q, k, v
+
+
+def _prefill(q, k, v):
+    out = torch.full_like(q, float("nan"))
+    _hip.prefill_attention(out, q, k, v)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("tokens", [333, 2048])
+def test_prompt_attention_exact_properties(device, tokens):
+    """For the causal prompt kernel (P is rounded to fp16 before its product with V, the
+    rest fp32): doubling V doubles the outputs, swapping two kv heads with their query
+    heads swaps the output heads, and 2q with k/2 changes no bit."""
+    _say("prompt attention exact properties", tokens)
+    q, k, v = _prompt(device, tokens, 70 + tokens)
+    floor = torch.where(k < 0, -(2.0**-13), 2.0**-13).to(torch.float16)
+    k = torch.where(k.abs() < 2.0**-13, floor, k).contiguous()
+    out = _prefill(q, k, v)
+    assert not torch.isnan(out).any()
+    doubled = _prefill(q, k, (v * 2).contiguous())
+    normal = out.abs() >= SUBNORMAL
+    assert torch.equal(doubled[normal], (out * 2)[normal])
+    tiny = (doubled[~normal].float() - (out * 2)[~normal].float()).abs()
+    assert tiny.numel() == 0 or float(tiny.max()) <= 2.0**-24
+    order = [3, 1, 2, 0]
+    qorder = [8 * order[g] + i for g in range(4) for i in range(8)]
+    swapped = _prefill(q[:, qorder].contiguous(), k[:, order].contiguous(), v[:, order].contiguous())
+    assert torch.equal(swapped, out[:, qorder])
+    scaled = _prefill((q * 2).contiguous(), (k * 0.5).contiguous(), v)
+    assert torch.equal(scaled, out)
