@@ -152,3 +152,52 @@ def test_rope_kv_append_parts_equals_the_fp16_path(device, tokens, splits):
         results.append((query, keys, values, pool))
     for a, b in zip(*results):
         assert np.array_equal(_bits(a), _bits(b))
+
+
+# --- exact properties at the decode step's shapes ------------------------------------------
+
+
+@pytest.mark.parametrize("m,n,k,splits", [s for s in PARTIAL_SHAPES if s[0] == 128])
+def test_gemm_partials_permute_and_scale_exactly(device, m, n, k, splits):
+    """Permuting the activation rows permutes the partials' rows, permuting the weight rows
+    permutes their columns, and doubling the weight doubles them, all bit for bit: every
+    output element is the same sequence of MFMA sums wherever its row and column sit in
+    the tiles, and a power-of-two scale rounds nothing."""
+    x, w = _inputs(device, m, n, k, seed=7 * n + k)
+    gen = torch.Generator(device="cpu").manual_seed(n + splits)
+    rows, cols = torch.randperm(m, generator=gen).to(device), torch.randperm(n, generator=gen).to(device)
+
+    def run(xx, ww):
+        out = torch.full((splits, m, n), float("nan"), dtype=torch.float32, device=device)
+        _hip.gemm_m128(out, xx.contiguous(), ww.contiguous(), splits=splits, epilogue=_hip.GEMM_PARTIALS)
+        torch.cuda.synchronize()
+        return out
+
+    base = run(x, w)
+    assert not torch.isnan(base).any()
+    assert torch.equal(run(x[rows], w), base[:, rows])
+    assert torch.equal(run(x, w[cols]), base[:, :, cols])
+    assert torch.equal(run(x, w * 2), base * 2)
+
+
+def test_gemm_swiglu_permutes_exactly(device):
+    """The SwiGLU epilogue (output column c from gate row c and up row half + c): the same
+    permutation of the gate rows and of the up rows permutes the output columns, and
+    permuting the activation rows permutes the output rows, bit for bit."""
+    m, n, k = 128, 11264, 2048
+    half = n // 2
+    x, w = _inputs(device, m, n, k, seed=91)
+    gen = torch.Generator(device="cpu").manual_seed(92)
+    rows, cols = torch.randperm(m, generator=gen).to(device), torch.randperm(half, generator=gen).to(device)
+
+    def run(xx, ww):
+        out = torch.full((m, half), float("nan"), dtype=torch.float16, device=device)
+        _hip.gemm_m128(out, xx.contiguous(), ww.contiguous(), epilogue=_hip.GEMM_SWIGLU)
+        torch.cuda.synchronize()
+        return out
+
+    base = run(x, w)
+    assert not torch.isnan(base).any()
+    assert torch.equal(run(x[rows], w), base[rows])
+    permuted = torch.cat((w[:half][cols], w[half:][cols]))
+    assert torch.equal(run(x, permuted), base[:, cols])
