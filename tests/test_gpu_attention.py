@@ -3,7 +3,7 @@
 The reference's attention tests (tests/unit/test_attention.py, tests/gpu/test_attention_cuda.py)
 re-run against the HIP path through the unchanged Python API, plus the batched shapes the
 hot path is measured on. Tolerance: max |gpu - expected| <= 2e-3 on the fp16 outputs with
-no relative term (the north star's bound; the reference's own tests use assert_close with
+no relative term (the parity bound of this path; the reference's own tests use assert_close with
 atol = rtol = 2e-3, which is looser), against both the op-for-op oracle (an fp16 output)
 and FP64 dense attention (compared unrounded); tighter where the reference uses a tighter
 bound. Each check prints the largest error it saw.
