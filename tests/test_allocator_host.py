@@ -823,3 +823,14 @@ def test_staged_prompt_append_checks_before_staging(tokens, error, needle):
     with pytest.raises(KeyError):
         with allocator.append_prompt(RequestId("unknown"), 3):
             pass
+
+
+def test_cached_lengths_checks_once_and_raises_for_an_unknown_request():
+    allocator = cpu_allocator(torch.zeros((22, 2, 8, 16, 4, 64), dtype=torch.float16))
+    for name, tokens in (("a", 5), ("b", 17)):
+        allocator.create(KVReservation(RequestId(name), 2))
+        allocator.append(RequestId(name), *kv_values(tokens))
+    assert allocator.cached_lengths((RequestId("b"), RequestId("a"))) == (17, 5)
+    assert allocator.cached_lengths(()) == ()
+    with pytest.raises(KeyError):
+        allocator.cached_lengths((RequestId("a"), RequestId("missing")))
