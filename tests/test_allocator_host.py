@@ -15,6 +15,7 @@ from math import ceil
 from typing import Any
 from unittest.mock import Mock
 
+import numpy as np
 import pytest
 import torch
 from hypothesis import settings
@@ -834,3 +835,31 @@ def test_cached_lengths_checks_once_and_raises_for_an_unknown_request():
     assert allocator.cached_lengths(()) == ()
     with pytest.raises(KeyError):
         allocator.cached_lengths((RequestId("a"), RequestId("missing")))
+
+
+def test_staged_decode_view_matches_each_staged_sequence():
+    """The host view of a staged decode step (tables, lengths, new-token slots and
+    positions) row by row, including a request whose new token takes a fresh block and
+    zero padding to a wider table."""
+    allocator = cpu_allocator(torch.zeros((22, 2, 16, 16, 4, 64), dtype=torch.float16))
+    names = {"a": 5, "b": 16, "c": 33, "d": 1}  # b's new token starts its second block
+    for name, tokens in names.items():
+        allocator.create(KVReservation(RequestId(name), 4))
+        allocator.append(RequestId(name), *kv_values(tokens))
+    order = (RequestId("c"), RequestId("b"), RequestId("d"), RequestId("a"))
+    with allocator.append_decode(order):
+        staged = allocator.staged_decode(order, width=6)
+        with pytest.raises(ValueError, match="wider"):
+            allocator.staged_decode(order, width=2)
+        for row, rid in enumerate(order):
+            length = names[rid] + 1
+            blocks = allocator._decode_appends[rid].sequence.blocks
+            assert len(blocks) == (length + 15) // 16
+            assert staged.lengths[row] == length and staged.positions[row] == length - 1
+            assert staged.tables[row].tolist() == list(blocks) + [0] * (6 - len(blocks))
+            assert staged.slots[row] == blocks[(length - 1) // 16] * 16 + (length - 1) % 16
+        assert staged.tables.dtype == np.int32 and staged.lengths.dtype == np.int32
+        assert staged.slots.dtype == np.int64 and staged.positions.dtype == np.int64
+        for layer in range(22):
+            kv = torch.zeros(len(order), 4, 64, dtype=torch.float16)
+            allocator.write_decode_layers(order, layer, kv, kv)
