@@ -241,8 +241,10 @@ def _check_weights(weights: TinyLlamaWeights, what: str) -> None:
 # projections on pc_gemm_m128: q|k|v, o_proj and down as fp32 split-K partial sums (summed
 # and rounded once by the RoPE / residual-add consumers), gate|up with the SwiGLU epilogue.
 # Shapes the kernel does not take (more rows, K not a multiple of 64, ...) use F.linear.
+# Split counts measured on the batch-128 step: q|k|v at 2 (160 workgroups of 32-row tiles,
+# half the partials of 4) 1.930 vs 1.950 ms; o_proj at 2 or 8 and down at 4 or 16 no better.
 GEMM_M128_ROWS = 128
-QKV_SPLITS = 4
+QKV_SPLITS = 2
 O_PROJ_SPLITS = 4
 DOWN_SPLITS = 8
 
