@@ -33,6 +33,7 @@ import weakref
 from dataclasses import dataclass
 from typing import Dict, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 from torch import Tensor
@@ -374,7 +375,9 @@ class DecodeGraph:
     exit at once). Per step the host does the allocator's staged-append bookkeeping, builds
     the plan into a pinned buffer, uploads the rows in use (and the empty rows that replace
     a longer previous plan) with two asynchronous copies and replays the graph; nothing
-    synchronizes.
+    synchronizes. step() takes the token ids from the device and returns a copy of the
+    logits; greedy() takes them from the host, in the first of the two copies, and returns
+    only each row's argmax (what a greedy loop reads back).
 
     Device faults fail closed. After each replay the attention workspace's fault word is
     copied to pinned memory. check_faults() raises AttentionFaultError if the last step's
@@ -494,6 +497,44 @@ class DecodeGraph:
             raise ValueError("input_ids must be int64 [batch, 1] matching request IDs")
         if input_ids.device != self._weights.embedding.device:
             raise ValueError("input_ids and weights must be on the same device")
+        rows = self._replay(request_ids, None, input_ids[:, 0], None)
+        return self._logits[:rows].clone().unsqueeze(1)
+
+    @torch.inference_mode()
+    def greedy(
+        self, token_ids: np.ndarray, request_ids: Tuple[RequestId, ...], device_token: Optional[Tuple[int, Tensor]] = None
+    ) -> Tensor:
+        """The same step for a greedy caller: the input ids come from the host (int64
+        [len(request_ids)], each below the vocabulary size), uploaded with the slots and
+        positions in one copy, except that `device_token` = (row, 0-dim int64 device
+        tensor) supplies row's id from device memory. Returns int64 [len(request_ids)] on
+        the device: the argmax of each row's logits, computed from the graph's own logits
+        buffer (no copy of the logits); check_faults() as for step()."""
+        request_ids = tuple(request_ids)
+        ids = np.asarray(token_ids)
+        if ids.dtype != np.int64 or ids.shape != (len(request_ids),):
+            raise ValueError("token_ids must be int64 [batch] matching request IDs")
+        if ids.size and (int(ids.min()) < 0 or int(ids.max()) >= self._weights.embedding.shape[0]):
+            raise ValueError("token ids must be below the vocabulary size")
+        if device_token is not None:
+            row, token = device_token
+            if type(row) is not int or not 0 <= row < len(request_ids):
+                raise ValueError("device_token row outside the batch")
+            if token.dtype != torch.int64 or token.numel() != 1 or token.device != self._weights.embedding.device:
+                raise ValueError("device_token must be one int64 id on the weights' device")
+        rows = self._replay(request_ids, ids, None, device_token)
+        return self._logits[:rows].argmax(-1)
+
+    def _replay(
+        self,
+        request_ids: Tuple[RequestId, ...],
+        host_ids: Optional[np.ndarray],
+        device_ids: Optional[Tensor],
+        device_token: Optional[Tuple[int, Tensor]],
+    ) -> int:
+        """Stage the step (allocator bookkeeping, pinned inputs, the plan) and replay the
+        graph; the ids come from `host_ids` (then `device_token` may replace one) or from
+        the device vector `device_ids`. Returns the number of real rows."""
         rows = len(request_ids)
         if not 1 <= rows <= self.batch:
             raise ValueError(f"this decode graph runs batches of 1 to {self.batch} requests")
@@ -507,6 +548,9 @@ class DecodeGraph:
             host64, host32 = self._host[turn]
             h64 = host64.numpy()
             h32 = host32.numpy()
+            if host_ids is not None:
+                h64[0, :rows] = host_ids
+                h64[0, rows:] = 0  # padding rows: a valid id, whose logits are dropped
             h64[1, :rows] = staged.slots
             h64[1, rows:] = -1  # padding rows: no slot, position 0, context length 0
             h64[2, :rows] = staged.positions
@@ -519,9 +563,14 @@ class DecodeGraph:
             self._host_rows[turn] = count
             upload = self._lens_span + max(count, self._device_rows) * self._fields
             self._device_rows = count
-            self._inputs64[1:].copy_(host64[1:], non_blocking=True)
+            if host_ids is not None:
+                self._inputs64.copy_(host64, non_blocking=True)
+                if device_token is not None:
+                    self._inputs64[0, device_token[0]].copy_(device_token[1].reshape(()))
+            else:
+                self._inputs64[1:].copy_(host64[1:], non_blocking=True)
+                self._inputs64[0, :rows].copy_(device_ids)
             self._inputs32[:upload].copy_(host32[:upload], non_blocking=True)
-            self._inputs64[0, :rows].copy_(input_ids[:, 0])
             self._graph.replay()
             self._fault_host[turn].copy_(_hip.fault_word(self._workspace), non_blocking=True)
             finished = torch.cuda.Event()
@@ -529,8 +578,7 @@ class DecodeGraph:
             self._finished[turn] = finished
             self._last_turn = turn
             allocator.record_decode_writes(request_ids, LAYERS)
-            logits = self._logits[:rows].clone()
-        return logits.unsqueeze(1)
+        return rows
 
 
 # ---------------------------------------------------------------------------------------
@@ -619,8 +667,9 @@ class PrefillGraph:
     padded at the end; causal attention keeps every real row blind to the padding rows
     after it, and a padding row's slot is -1, so it writes nothing to the pool. Per call
     the host stages the append (KVAllocator.append_prompt, same checks, errors and
-    publish-after-forward semantics as prefill_paged), copies the inputs into the static
-    buffers and replays the graph; nothing synchronizes.
+    publish-after-forward semantics as prefill_paged), uploads the inputs into the static
+    buffers with one copy from pinned memory (the ids from the device for step(), from the
+    host, in the same copy, for greedy()) and replays the graph; nothing synchronizes.
 
     The GEMMs run at `tokens` rows, and the LM head on the last row alone, so logits and
     cache bytes may differ from prefill_paged's in the last bits, as between any two GEMM
@@ -643,6 +692,11 @@ class PrefillGraph:
         self._inputs[1].fill_(-1)  # warm-up and capture write nothing to the pool
         self._inputs[2].copy_(torch.arange(tokens, device=device))
         self._inputs[3, 0] = tokens - 1
+        # Two pinned staging buffers of the same layout used in turn; an event recorded
+        # after a buffer's upload marks when it may be refilled.
+        self._host = [self._inputs.cpu().pin_memory() for _ in range(2)]
+        self._uploaded: list = [None, None]
+        self._turn = 0
         stream = torch.cuda.current_stream(device)
         self._forward()  # eager warm-up: library initialisation and GEMM selection outside the capture
         torch.cuda.synchronize(device)
@@ -659,28 +713,69 @@ class PrefillGraph:
         x = _prefill_forward(ids, positions, slots, self._weights, self._allocator.pool, self._table)
         return F.linear(x.index_select(0, last[:1]), self._weights.lm_head)  # [1, vocab]
 
+    def _check_empty(self, request_id: RequestId) -> None:
+        if self._allocator.cached_length(request_id) != 0:
+            raise ValueError("paged prefill requires an empty request cache")
+
+    def _check_rows(self, rows: int) -> None:
+        if not 1 <= rows <= self.tokens:
+            raise ValueError(f"this prefill graph holds prompts of 1 to {self.tokens} positions")
+
+    def _replay(self, request_id: RequestId, rows: int, host_ids: Optional[np.ndarray],
+                device_ids: Optional[Tensor]) -> None:
+        """Stage the append, upload the slots (and the host ids, when given) with the last
+        row's index in one copy from a pinned buffer, and replay the graph."""
+        with self._allocator.append_prompt(request_id, rows) as staged:
+            turn = self._turn
+            self._turn ^= 1
+            if self._uploaded[turn] is not None:
+                self._uploaded[turn].synchronize()  # its previous upload has run
+            host = self._host[turn].numpy()
+            if host_ids is not None:
+                host[0, :rows] = host_ids  # rows past the prompt keep earlier valid ids
+            host[1, :rows] = staged.slots
+            host[1, rows:] = -1  # padding rows write nothing to the pool
+            host[3, 0] = rows - 1
+            if host_ids is not None:
+                self._inputs.copy_(self._host[turn], non_blocking=True)
+            else:
+                self._inputs[1:].copy_(self._host[turn][1:], non_blocking=True)
+                self._inputs[0, :rows].copy_(device_ids)
+            uploaded = torch.cuda.Event()
+            uploaded.record()
+            self._uploaded[turn] = uploaded
+            self._graph.replay()
+            for index in range(LAYERS):
+                staged.record_layer(index)
+
     @torch.inference_mode()
     def step(self, input_ids: Tensor, request_id: RequestId) -> Tensor:
         """prefill_paged(input_ids, weights, allocator, request_id) by graph replay for a
         prompt of 1 to `tokens` positions; returns fresh fp16 logits [1, 1, vocab] of the
         prompt's last position."""
-        allocator = self._allocator
-        if allocator.cached_length(request_id) != 0:
-            raise ValueError("paged prefill requires an empty request cache")
+        self._check_empty(request_id)
         if input_ids.dtype != torch.int64 or input_ids.ndim != 2 or input_ids.shape[0] != 1:
             raise ValueError("input_ids must be int64 [1, tokens]")
         if input_ids.device != self._weights.embedding.device:
             raise ValueError("input_ids and weights must be on the same device")
         rows = input_ids.shape[1]
-        if not 1 <= rows <= self.tokens:
-            raise ValueError(f"this prefill graph holds prompts of 1 to {self.tokens} positions")
-        with allocator.append_prompt(request_id, rows) as staged:
-            self._inputs[0, :rows].copy_(input_ids[0])
-            self._inputs[1, :rows].copy_(staged.slot_mapping)
-            self._inputs[1, rows:].fill_(-1)
-            self._inputs[3, :1].fill_(rows - 1)
-            self._graph.replay()
-            for index in range(LAYERS):
-                staged.record_layer(index)
-            logits = self._logits.clone()
-        return logits.unsqueeze(0)
+        self._check_rows(rows)
+        self._replay(request_id, rows, None, input_ids[0])
+        return self._logits.clone().unsqueeze(0)
+
+    @torch.inference_mode()
+    def greedy(self, prompt_ids: np.ndarray, request_id: RequestId) -> Tensor:
+        """The same prefill for a greedy caller, from host token ids (int64 [tokens], each
+        below the vocabulary size) uploaded with the slots in one copy. Returns the argmax
+        of the last position's logits as a 0-dim int64 device tensor (the greedy first
+        token), computed from the graph's own logits buffer."""
+        self._check_empty(request_id)
+        ids = np.asarray(prompt_ids)
+        if ids.dtype != np.int64 or ids.ndim != 1:
+            raise ValueError("prompt_ids must be int64 [tokens]")
+        rows = ids.shape[0]
+        self._check_rows(rows)
+        if int(ids.min()) < 0 or int(ids.max()) >= self._weights.embedding.shape[0]:
+            raise ValueError("token ids must be below the vocabulary size")
+        self._replay(request_id, rows, ids, None)
+        return self._logits[0].argmax()

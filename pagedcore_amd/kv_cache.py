@@ -129,16 +129,38 @@ class _HostOnlyWriter:
         )
 
 
-@dataclass
+@dataclass(eq=False)
 class StagedPrompt:
     """A prompt append staged by KVAllocator.append_prompt: the caller writes each layer's
-    K/V to `slot_mapping` itself and records it with record_layer, in layer order."""
+    K/V to `slot_mapping` itself and records it with record_layer, in layer order.
+
+    `slots` holds the slot mapping on the host; `slot_mapping` and `positions` are its
+    device copies, uploaded together on first use (a caller that stages its inputs itself,
+    such as a graph replay, reads `slots` and uploads nothing here)."""
 
     request_id: RequestId
     tokens: int
-    slot_mapping: Tensor  # int64 [tokens]: block * 16 + offset of each new position
-    positions: Tensor  # int64 [tokens]: the new positions (cached length .. + tokens - 1)
+    slots: np.ndarray  # int64 [tokens]: block * 16 + offset of each new position
+    start: int  # the first new position (the cached length before the append)
+    device: torch.device
     written_layers: int = 0
+    _uploaded: Optional[Tensor] = None
+
+    def _device_rows(self) -> Tensor:
+        if self._uploaded is None:
+            positions = np.arange(self.start, self.start + self.tokens, dtype=np.int64)
+            self._uploaded = _upload(np.stack([self.slots, positions]), self.device)
+        return self._uploaded
+
+    @property
+    def slot_mapping(self) -> Tensor:
+        """int64 [tokens] on the pool's device: block * 16 + offset of each new position."""
+        return self._device_rows()[0]
+
+    @property
+    def positions(self) -> Tensor:
+        """int64 [tokens] on the pool's device: the new positions (start .. + tokens - 1)."""
+        return self._device_rows()[1]
 
     def record_layer(self, layer_index: int) -> None:
         if type(layer_index) is not int or layer_index != self.written_layers or layer_index >= LAYERS:
@@ -401,10 +423,8 @@ class KVAllocator:
             raise RuntimeError("KV pool has insufficient free blocks")
         new_blocks = tuple(reversed(self._free_blocks[-additional:])) if additional else ()
         blocks = sequence.blocks + new_blocks
-        slots = _slot_mapping(blocks, sequence.length, tokens)
-        positions = np.arange(sequence.length, length, dtype=np.int64)
-        both = _upload(np.stack([slots, positions]), self._pool.device)
-        staged = StagedPrompt(request_id, tokens, both[0], both[1])
+        staged = StagedPrompt(request_id, tokens, _slot_mapping(blocks, sequence.length, tokens), sequence.length,
+                              self._pool.device)
         self._prompt_append = staged
         self._touch()
         try:

@@ -28,8 +28,10 @@ tokens, in the order of the plan (the prefill token first): the decode step's ho
 then runs while the GPU executes the prefill. Only when that token can end the request
 early, an EOS with ignore_eos off, does the host wait for it before forming the batch, as
 the batch must not hold a finished request. Inputs go to the device through pinned memory
-without blocking, and the selected tokens come back with one asynchronous copy and one
-event wait.
+without blocking (with the captured graphs, each replay's ids, slots and plan in one or two
+copies), the graphs hand back each row's argmax rather than a copy of the logits, and the
+selected ids come back by asynchronous copies into one pinned buffer (the first token's
+enqueued right after its prefill) and one event wait.
 
 A device-side failure fails closed (the reference's rule for unsafe device failures,
 docs/DESIGN.md:178,255,282): when a decode step's paged attention reports a fault (its
@@ -45,6 +47,7 @@ from dataclasses import dataclass, field
 from enum import Enum
 from typing import Callable, Deque, Dict, List, Optional, Sequence, Tuple, Union
 
+import numpy as np
 import torch
 from torch import Tensor
 
@@ -167,12 +170,16 @@ class DecodeWorker:
         self._graphs: Dict[int, object] = {}
         self._prompt_sizes = tuple(sorted(set(prompt_sizes)))
         self._prefill_graphs: Dict[int, object] = {}
-        self._pending: Deque[GenerationRequest] = deque()
+        # Waiting requests, each with its prompt as an int64 array (converted once, at
+        # submit, off the iteration's critical path).
+        self._pending: Deque[Tuple[GenerationRequest, np.ndarray]] = deque()
         self._active: Dict[RequestId, _Active] = {}
         self._cancelled: set = set()
         self._results: Dict[RequestId, GreedyResult] = {}
         self._known: set = set()
         self._fault: Optional[AttentionFaultError] = None
+        self._host_tokens: Optional[Tensor] = None  # pinned read-back buffer of selected ids
+        self._read_back_end = 0  # ids copied into it this iteration
 
     # -- queue -----------------------------------------------------------------------------
 
@@ -186,7 +193,7 @@ class DecodeWorker:
         if request.block_credits > self._allocator.pool.shape[2]:
             raise ValueError("request exceeds total KV pool capacity")
         self._known.add(request.request_id)
-        self._pending.append(request)
+        self._pending.append((request, np.fromiter(request.input_ids, dtype=np.int64, count=len(request.input_ids))))
 
     def cancel(self, request_id: RequestId) -> None:
         """Stop a waiting or active request; its resources go at the next cleanup."""
@@ -204,7 +211,7 @@ class DecodeWorker:
 
     @property
     def pending_ids(self) -> Tuple[RequestId, ...]:
-        return tuple(r.request_id for r in self._pending)
+        return tuple(r.request_id for r, _ in self._pending)
 
     @property
     def results(self) -> Dict[RequestId, GreedyResult]:
@@ -229,6 +236,7 @@ class DecodeWorker:
 
     def _iterate(self) -> List[Tuple[RequestId, int]]:
         self._cleanup()
+        self._read_back_end = 0
         emitted: List[Tuple[RequestId, int]] = []
         first = self._admit_one()  # (admitted request, its first token on the device)
         if first is not None:
@@ -243,15 +251,14 @@ class DecodeWorker:
             for rid, state in self._active.items()
             if state.finish is None and (first is None or rid != first[0] or state.request.max_new_tokens > 1)
         )
-        chosen: List[Tensor] = [] if first is None else [first[1].view(1)]
+        chosen: List[Tensor] = []
+        if first is not None:
+            chosen.append(self._read_back(first[1].view(1)))  # enqueued before the decode step
         graph = None
         if batch:
-            tokens = self._batch_tokens(batch)
-            if first is not None and first[0] in batch:
-                tokens[batch.index(first[0]), 0] = first[1]  # the prefill's selection, device to device
-            logits, graph = self._decode_batch(tokens, batch)
-            chosen.append(logits[:, -1].argmax(dim=-1))
-        values = self._fetch(torch.cat(chosen)) if chosen else []
+            selected, graph = self._decode_batch(batch, first)
+            chosen.append(self._read_back(selected))
+        values = self._fetch(chosen)
         if graph is not None:
             graph.check_faults()  # decode_paged checks inside its step
         if first is not None:
@@ -272,17 +279,31 @@ class DecodeWorker:
             return host.to(device)
         return host.pin_memory().to(device, non_blocking=True)
 
-    def _fetch(self, values: Tensor) -> List[int]:
-        """Host copy of a small device int64 vector: one asynchronous copy to pinned memory
-        and a wait on an event recorded after it (other streams keep running)."""
+    def _read_back(self, values: Tensor) -> Tensor:
+        """Enqueue the copy of selected ids (an int64 vector on the pool's device) into the
+        pinned read-back buffer, after the ids already copied this iteration; returns the
+        host tensor _fetch reads. The buffer is reused every iteration, and _fetch waits for
+        the copies before anything reads it."""
         if values.device.type != "cuda":
-            return [int(v) for v in values.tolist()]
-        host = torch.empty(values.shape, dtype=values.dtype, pin_memory=True)
-        host.copy_(values, non_blocking=True)
-        done = torch.cuda.Event()
-        done.record()
-        done.synchronize()
-        return host.tolist()
+            return values
+        if self._host_tokens is None:
+            self._host_tokens = torch.empty(self._max_active + 1, dtype=torch.int64, pin_memory=True)
+        start = self._read_back_end
+        end = start + values.numel()
+        if end > self._host_tokens.numel():
+            raise RuntimeError("more selected ids than the read-back buffer holds")
+        self._host_tokens[start:end].copy_(values, non_blocking=True)
+        self._read_back_end = end
+        return self._host_tokens[start:end]
+
+    def _fetch(self, chosen: List[Tensor]) -> List[int]:
+        """The ids of this iteration's _read_back calls, in order, after one wait on an
+        event recorded behind their copies (other streams keep running)."""
+        if self._read_back_end:
+            done = torch.cuda.Event()
+            done.record()
+            done.synchronize()
+        return [int(v) for part in chosen for v in part.tolist()]
 
     def run(self, max_steps: Optional[int] = None) -> Dict[RequestId, GreedyResult]:
         """Iterate until every submitted request finished (and was cleaned up)."""
@@ -306,14 +327,14 @@ class DecodeWorker:
             if state.finish is not None:
                 self._results[rid] = self._result(state)
         if self._cancelled:
-            self._pending = deque(r for r in self._pending if r.request_id not in self._cancelled)
+            self._pending = deque(item for item in self._pending if item[0].request_id not in self._cancelled)
 
     def _admit_one(self) -> Optional[Tuple[RequestId, Tensor]]:
         """Admit and prefill the queue head if it fits; returns it with its first token
         still on the device (argmax of the prompt's last logits), or None."""
         if not self._pending or len(self._active) >= self._max_active:
             return None
-        request = self._pending[0]
+        request, prompt = self._pending[0]
         counts = self._allocator.capacity()
         if request.block_credits > counts.total_blocks - counts.reserved_blocks:
             return None  # waits (strict FIFO: nothing behind it is admitted first)
@@ -322,15 +343,14 @@ class DecodeWorker:
         self._allocator.create(KVReservation(rid, request.block_credits))
         self._active[rid] = _Active(request)
         try:
-            device = self._device()
-            ids = torch.tensor([list(request.input_ids)], dtype=torch.int64)
-            ids = ids.pin_memory().to(device, non_blocking=True) if device.type == "cuda" else ids.to(device)
-            size = next((size for size in self._prompt_sizes if size >= len(request.input_ids)), None)
+            size = next((size for size in self._prompt_sizes if size >= len(prompt)), None)
             if size is not None:
-                logits = self._prefill_graph_for(size).step(ids, rid)
+                token = self._prefill_graph_for(size).greedy(prompt, rid)
             else:
-                logits = self._prefill(ids, self._weights, self._allocator, rid)
-            token = logits[0, -1].argmax()
+                device = self._device()
+                ids = torch.tensor(prompt, dtype=torch.int64).view(1, -1)
+                ids = ids.pin_memory().to(device, non_blocking=True) if device.type == "cuda" else ids.to(device)
+                token = self._prefill(ids, self._weights, self._allocator, rid)[0, -1].argmax()
         except BaseException:
             # A failed admission leaves nothing behind: the request leaves the active set
             # and its reservation (with any blocks a partial prefill published) is
@@ -364,13 +384,25 @@ class DecodeWorker:
         for size in self._prompt_sizes:
             self._prefill_graph_for(size)
 
-    def _decode_batch(self, tokens: Tensor, batch: Tuple[RequestId, ...]):
-        """The step's logits, and the DecodeGraph that ran it (None for eager decoding)."""
+    def _decode_batch(self, batch: Tuple[RequestId, ...], first: Optional[Tuple[RequestId, Tensor]]):
+        """The step's selected ids (int64 [len(batch)] on the device), and the DecodeGraph
+        that ran it (None for eager decoding). Each request's input is its last selected
+        id; `first`'s is still on the device (the prefill's selection, fed device to
+        device)."""
+        row = batch.index(first[0]) if first is not None and first[0] in batch else None
         size = next((size for size in self._graph_sizes if size >= len(batch)), None)
         if size is not None:
             graph = self._graph_for(size)
-            return graph.step(tokens, batch), graph
-        return self._decode(tokens, self._weights, self._allocator, batch), None
+            ids = np.fromiter(
+                (self._active[rid].selected[-1] if self._active[rid].selected else 0 for rid in batch),
+                dtype=np.int64,
+                count=len(batch),
+            )
+            return graph.greedy(ids, batch, None if row is None else (row, first[1])), graph
+        tokens = self._batch_tokens(batch)
+        if row is not None:
+            tokens[row, 0] = first[1]
+        return self._decode(tokens, self._weights, self._allocator, batch)[:, -1].argmax(dim=-1), None
 
     def _select(self, rid: RequestId, token: int, emitted: List[Tuple[RequestId, int]]) -> None:
         state = self._active[rid]

@@ -532,6 +532,71 @@ def test_prefill_graph_matches_prefill_paged(device):
     assert graphed.capacity().owned_blocks == counts.owned_blocks
 
 
+def test_graph_greedy_paths_equal_step_argmax(device):
+    """PrefillGraph.greedy and DecodeGraph.greedy (host ids in, each row's argmax out) on
+    one pool against step() followed by argmax on a twin pool: the same selected ids, the
+    same pool bytes and allocator state, over prompts of several lengths and decode steps
+    of 2, 5 and 3 rows (padding) with one row's id taken from the device, eager GPU work
+    between replays. Bad ids are rejected before anything is staged."""
+    weights = _synthetic(device)
+    pools = [torch.full((22, 2, 60, 16, 4, 64), float("nan"), dtype=torch.float16, device=device) for _ in range(2)]
+    by_step, by_greedy = (KVAllocator(pool) for pool in pools)
+    prefills = [dec.PrefillGraph(weights, allocator, 64) for allocator in (by_step, by_greedy)]
+    requests = [RequestId(f"s{index}") for index in range(5)]
+    first = {}
+    for index, (request, length) in enumerate(zip(requests, (1, 9, 16, 40, 64))):
+        for allocator in (by_step, by_greedy):
+            allocator.create(KVReservation(request, (length + 8 + 15) // 16))
+        prompt = (np.arange(length, dtype=np.int64) * 7 + index) % 31
+        logits = prefills[0].step(torch.from_numpy(prompt).view(1, -1).to(device), request)
+        token = prefills[1].greedy(prompt, request)
+        torch.cuda.synchronize()
+        assert token.dtype == torch.int64 and token.ndim == 0
+        assert int(token) == int(logits[0, 0].argmax())
+        first[request] = token
+        torch.randn(1000, device=device).sum().item()  # unrelated eager work between replays
+    assert torch.equal(pools[0].view(torch.int16), pools[1].view(torch.int16))
+    assert by_step.capacity() == by_greedy.capacity()
+    spare = RequestId("spare")
+    by_greedy.create(KVReservation(spare, 1))
+    with pytest.raises(ValueError, match="vocabulary"):
+        prefills[1].greedy(np.array([3, 31], dtype=np.int64), spare)
+    with pytest.raises(ValueError, match="int64"):
+        prefills[1].greedy(np.array([3, 4], dtype=np.int32), spare)
+    assert by_greedy.cached_length(spare) == 0
+    by_greedy.release_all(spare)
+
+    decodes = [dec.DecodeGraph(weights, allocator, 5) for allocator in (by_step, by_greedy)]
+    for step, rows in enumerate((2, 5, 3)):
+        order = tuple(requests[(step + row) % 5] for row in range(rows))
+        ids = np.array([(4 * step + row) % 31 for row in range(rows)], dtype=np.int64)
+        row = rows - 1  # this row's id comes from the device: its prefill's selection
+        tokens = torch.from_numpy(ids.copy()).view(-1, 1).to(device)
+        tokens[row, 0] = first[order[row]]
+        expected = decodes[0].step(tokens, order)[:, -1].argmax(-1)
+        got = decodes[1].greedy(ids, order, (row, first[order[row]]))
+        torch.cuda.synchronize()
+        decodes[0].check_faults()
+        decodes[1].check_faults()
+        assert got.dtype == torch.int64 and got.shape == (rows,)
+        assert torch.equal(got, expected)
+        assert torch.equal(pools[0].view(torch.int16), pools[1].view(torch.int16))
+        assert by_step.capacity() == by_greedy.capacity()
+        assert [by_greedy.cached_length(r) for r in order] == [by_step.cached_length(r) for r in order]
+        torch.randn(1000, device=device).sum().item()
+    lengths = [by_greedy.cached_length(r) for r in requests]
+    for bad, match in (
+        (np.array([0, 31], dtype=np.int64), "vocabulary"),
+        (np.array([0, 1, 2], dtype=np.int64), "matching request IDs"),
+        (np.array([0, 1], dtype=np.int32), "matching request IDs"),
+    ):
+        with pytest.raises(ValueError, match=match):
+            decodes[1].greedy(bad, tuple(requests[:2]))
+    with pytest.raises(ValueError, match="outside the batch"):
+        decodes[1].greedy(np.array([0, 1], dtype=np.int64), tuple(requests[:2]), (2, first[requests[0]]))
+    assert [by_greedy.cached_length(r) for r in requests] == lengths
+
+
 # ---------------------------------------------------------------------------------------
 # Prompt attention (pc_prefill_attention)
 # ---------------------------------------------------------------------------------------

@@ -6,6 +6,7 @@ bookkeeping (appends and staged decode writes through the CPU test writer)."""
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -58,6 +59,17 @@ def _worker(model, blocks=32, max_active=2):
 
 def _request(name, prompt=5, new=4, **kw):
     return GenerationRequest(RequestId(name), tuple(range(1, prompt + 1)), new, **kw)
+
+
+def _greedy_decode(step, ids, rids, device_token):
+    """A fake decode graph's greedy(): its step() over the host ids (with device_token's
+    row replaced), argmax of each row."""
+    assert ids.dtype == np.int64 and ids.shape == (len(rids),)
+    tokens = torch.from_numpy(ids.copy()).view(-1, 1)
+    if device_token is not None:
+        row, token = device_token
+        tokens[row, 0] = token
+    return step(tokens, rids)[:, -1].argmax(dim=-1)
 
 
 def _submit(worker, model, requests):
@@ -221,6 +233,9 @@ def test_decode_steps_replay_the_smallest_graph_that_holds_the_batch(monkeypatch
             used.append((self.batch, len(rids)))
             return model.decode(tokens, None, self.allocator, rids)
 
+        def greedy(self, ids, rids, device_token=None):
+            return _greedy_decode(self.step, ids, rids, device_token)
+
         def check_faults(self):
             pass
 
@@ -264,6 +279,10 @@ def test_admissions_replay_the_smallest_prefill_graph_that_holds_the_prompt(monk
             assert ids.shape[1] <= self.tokens
             used.append((self.tokens, ids.shape[1]))
             return model.prefill(ids, None, self.allocator, rid)[:, -1:]
+
+        def greedy(self, prompt, rid):
+            assert prompt.dtype == np.int64 and prompt.ndim == 1
+            return self.step(torch.from_numpy(prompt.copy()).view(1, -1), rid)[0, -1].argmax()
 
     monkeypatch.setattr(decoder, "PrefillGraph", RecordingPrefillGraph)
     allocator = cpu_allocator(torch.zeros((22, 2, 32, 16, 4, 64), dtype=torch.float16))
@@ -310,6 +329,9 @@ def test_a_device_fault_stops_the_worker_before_it_emits(monkeypatch, where):
 
         def step(self, tokens, rids):
             return faulty_decode(tokens, None, self.allocator, rids)
+
+        def greedy(self, ids, rids, device_token=None):
+            return _greedy_decode(self.step, ids, rids, device_token)
 
         def check_faults(self):
             if len(steps) == 3:
