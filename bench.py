@@ -103,13 +103,7 @@ def run_decode(steps: int, warmup: int, use_graph: bool = True) -> dict:
 
     replay = layers.step
     if use_graph:
-        side = torch.cuda.Stream(device=device)
-        side.wait_stream(torch.cuda.current_stream(device))
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(graph, stream=side):
-                layers.step()
-        torch.cuda.current_stream(device).wait_stream(side)
+        graph = _captured(layers.step, device)
         for _ in range(3):
             layers.out.fill_(float("nan"))
             graph.replay()
@@ -187,14 +181,12 @@ def _check_faults(workspace: Tensor, where: str) -> None:
 
 
 def _captured(fn, device: torch.device) -> torch.cuda.CUDAGraph:
-    side = torch.cuda.Stream(device=device)
-    side.wait_stream(torch.cuda.current_stream(device))
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(side), torch.cuda.graph(graph, stream=side):
-        fn()
-    torch.cuda.current_stream(device).wait_stream(side)
-    torch.cuda.synchronize(device)
-    return graph
+    """fn's launches as a graph, captured without emptying torch's allocator cache (the
+    decoder's capture_graph: a cache released to the driver slows the next seconds'
+    bandwidth-bound kernels)."""
+    from pagedcore_amd.decoder import capture_graph
+
+    return capture_graph(fn, device)[0]
 
 
 def cpu_long_context_baseline(pool: Tensor, queries: Tensor, new_kv: Tensor, w: workloads.BatchedDecode,
@@ -813,31 +805,32 @@ def calibration_copy(mib: int, device: torch.device) -> None:
 
 def run_extra(selected: set, steps: int, cpu_seconds: float = 0.0) -> dict:
     """The workloads beside the headline, each reported as its own object (with a CPU
-    baseline of about `cpu_seconds` where the workload has one; 0 = none)."""
+    baseline of about `cpu_seconds` where the workload has one; 0 = none).
+
+    Device memory a workload frees stays in torch's cache for the next one: returning it to
+    the driver (torch.cuda.empty_cache) and allocating again slows the next workload's
+    bandwidth-bound kernels for several seconds (measured: the decode step ran 1.97 ms
+    instead of 1.92 right after an empty_cache, and 1.92 after 10 idle seconds or with no
+    empty_cache in between)."""
     extra = {}
     if "single_decode" in selected:
         extra["single_decode_c1"] = run_single_decode(cpu_seconds=cpu_seconds)
         print(f"single decode: {extra['single_decode_c1']}", file=sys.stderr, flush=True)
     if "prompt_append" in selected:
         extra["prompt_append"] = run_prompt_append(max(10, steps), cpu_seconds)
-        torch.cuda.empty_cache()
         print(f"prompt append: {extra['prompt_append']}", file=sys.stderr, flush=True)
     if "long_context" in selected:
         extra["long_context_b256"] = run_long_context(max(5, steps // 5), 2, cpu_seconds)
-        torch.cuda.empty_cache()
         print(f"long context: {extra['long_context_b256']}", file=sys.stderr, flush=True)
     if "decode_step" in selected:
         # ten untimed steps: the first replays of a fresh process run about 4 % slower
         extra["decode_step_b128"] = run_decode_step(max(10, steps // 2), 10)
-        torch.cuda.empty_cache()
         print(f"decode step: {extra['decode_step_b128']}", file=sys.stderr, flush=True)
     if "prefill" in selected:
         extra["prefill_2048"] = run_prefill(5)
-        torch.cuda.empty_cache()
         print(f"prefill: {extra['prefill_2048']}", file=sys.stderr, flush=True)
     if "serving" in selected:
         extra["serving"] = run_serving()
-        torch.cuda.empty_cache()
         print(f"serving: {extra['serving']}", file=sys.stderr, flush=True)
     return extra
 
@@ -896,8 +889,7 @@ def main() -> int:
         baseline = cpu_baseline(layers, args.cpu_seconds)
         baseline["with_allocator_bookkeeping"] = cpu_bookkeeping_baseline(layers, EXTRA_CPU_SECONDS)
         print(f"cpu baseline: {baseline}", file=sys.stderr, flush=True)
-    del layers, r["layers"]
-    torch.cuda.empty_cache()
+    del layers, r["layers"]  # its memory stays cached for the next workloads (see run_extra)
     extra = run_extra(selected, args.steps, 0.0 if args.no_cpu_baseline else EXTRA_CPU_SECONDS)
 
     record = {
