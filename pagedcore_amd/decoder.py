@@ -385,8 +385,13 @@ def capture_graph(fn: Callable[[], T], device: torch.device) -> Tuple[torch.cuda
         graph.capture_begin()
         try:
             result = fn()
-        finally:
-            graph.capture_end()
+        except BaseException:
+            try:
+                graph.capture_end()
+            except RuntimeError:
+                pass  # the capture is abandoned; fn's error is the one to report
+            raise
+        graph.capture_end()
     stream.wait_stream(side)
     torch.cuda.synchronize(device)
     return graph, result
