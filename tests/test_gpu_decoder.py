@@ -532,6 +532,26 @@ def test_prefill_graph_matches_prefill_paged(device):
     assert graphed.capacity().owned_blocks == counts.owned_blocks
 
 
+def test_capture_graph_replays_and_reports_the_callables_error(device):
+    """decoder.capture_graph (the graphs' capture, which leaves torch's allocator cache
+    alone): a capture whose callable raises reports that error and leaves the stream usable;
+    a normal capture's outputs are refreshed by every replay, with eager work in between."""
+    def failing():
+        torch.empty(4, device=device).fill_(1.0)  # a launch inside the capture
+        raise ValueError("inside the capture")
+
+    with pytest.raises(ValueError, match="inside the capture"):
+        dec.capture_graph(failing, device)
+    source = torch.zeros(4, device=device)
+    graph, out = dec.capture_graph(lambda: source * 2 + 1, device)
+    for value in (1.0, 5.0, -3.0):
+        source.fill_(value)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, torch.full((4,), 2 * value + 1, device=device))
+        torch.randn(1000, device=device).sum().item()  # unrelated eager work between replays
+
+
 def test_graph_greedy_paths_equal_step_argmax(device):
     """PrefillGraph.greedy and DecodeGraph.greedy (host ids in, each row's argmax out) on
     one pool against step() followed by argmax on a twin pool: the same selected ids, the
