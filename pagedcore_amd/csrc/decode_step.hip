@@ -247,6 +247,14 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(_Float16* __
   const int64_t base = static_cast<int64_t>(blockIdx.x) * width;
   const int tid = threadIdx.x;
   const int chunks = width / 8;
+  // The weight chunks are loaded first, with the same guards as their use below, so that
+  // their round trip overlaps the residual's instead of following the reduction.
+  half8_t wt[kNormMaxChunks];
+#pragma unroll
+  for (int k = 0; k < kNormMaxChunks; ++k) {
+    const int chunk = tid + k * kNormThreads;
+    if (chunk < chunks) wt[k] = *reinterpret_cast<const half8_t*>(weight + 8 * chunk);
+  }
   half8_t h[kNormMaxChunks];
   float squares = 0.0f;
 #pragma unroll
@@ -280,12 +288,11 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(_Float16* __
   for (int k = 0; k < kNormMaxChunks; ++k) {
     const int chunk = tid + k * kNormThreads;
     if (chunk < chunks) {
-      const half8_t w = *reinterpret_cast<const half8_t*>(weight + 8 * chunk);
       half8_t o;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float normalized = static_cast<float>(round_h(static_cast<float>(h[k][i]) * scale));
-        o[i] = round_h(static_cast<float>(w[i]) * normalized);
+        o[i] = round_h(static_cast<float>(wt[k][i]) * normalized);
       }
       *reinterpret_cast<half8_t*>(out + base + 8 * chunk) = o;
     }
