@@ -21,7 +21,6 @@ torch CPU path, timed on a bounded sample on this host's cores).
 from __future__ import annotations
 
 import argparse
-import ctypes
 import json
 import os
 import sys
