@@ -787,7 +787,8 @@ def test_staged_prompt_append_takes_the_blocks_append_would_and_publishes_after_
     assert staged_alloc.capacity() == plain.capacity()
     table = plain.block_table(request)
     expected = [table[p // 16] * 16 + p % 16 for p in range(5, 35)]
-    assert staged.slot_mapping.tolist() == expected
+    assert staged.slots.dtype == np.int64 and staged.slots.tolist() == expected  # the host copy
+    assert staged.slot_mapping.tolist() == expected  # the device copy, uploaded on first use
 
 
 def test_staged_prompt_append_discards_on_error_and_requires_every_layer():
