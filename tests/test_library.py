@@ -9,6 +9,8 @@ import re
 
 import numpy as np
 import pytest
+from hypothesis import given, settings
+from hypothesis import strategies as st
 
 from pagedcore_amd import _hip
 from tests.bin_plan import ROW, check_decode_plan
@@ -184,6 +186,26 @@ def test_decode_plan_edge_shapes(name, lengths, max_blocks):
         assert plan.shape[0] == 0
     else:
         assert plan.shape[0] % 8 == 0 and stats["rows"] == plan.shape[0]
+
+
+@settings(max_examples=60, deadline=None, derandomize=True)
+@given(
+    batch=st.integers(1, 300),
+    top=st.integers(1, 2048),
+    zeros=st.floats(0.0, 0.5),
+    seed=st.integers(0, 2**31 - 1),
+)
+def test_decode_plan_random_batches_pass_the_full_check(batch, top, zeros, seed):
+    """Random ragged batches (1 to 300 sequences, lengths up to `top`, a share of empty
+    rows): every plan passes the full check of what the kernel reads and writes, and fits
+    the advertised capacity and workspace."""
+    rng = np.random.default_rng(seed)
+    lengths = rng.integers(1, top + 1, size=batch).astype(np.int32)
+    lengths[rng.random(batch) < zeros] = 0
+    max_blocks = max(1, (int(lengths.max()) + 15) // 16)
+    tables = rng.integers(0, 1 << 20, size=(batch, max_blocks)).astype(np.int32)
+    plan, stats = _plan_and_check(lengths, tables, 1 << 20)
+    assert (plan.shape[0] == 0) == (lengths.max() == 0)
 
 
 def test_decode_plan_rejects_bad_arguments():
